@@ -1,0 +1,275 @@
+"""Benchmark of the MI355X quantized linear layer on BASELINE.json's headline configs.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+
+One step = one decode GEMV y[1, 11008] = x[1, 4096] . W^T over a Q4_0 weight
+W[11008, 4096] (the Llama-7B gate/up projection; BASELINE's "4096x11008 b=1").
+The weight is uploaded as >= 1 GiB of distinct copies and the steps rotate over
+them, so every step streams its 25.4 MB from HBM rather than from the 256 MB
+Infinity Cache.  Inputs are resident in HBM before timing starts.
+
+`value` = algorithmic bytes per step (W bytes + x + y) x steps / wall time of the
+timed region (HIP events on the launch stream, device synchronised on both sides).
+`roofline.achieved` uses the average duration of a single GEMV launch, from an
+event pair around each launch over a second timed pass.  The Q8_0 prefill GEMM
+(W[11008, 4096], M = 512, bf16 X) is measured the same way and reported under
+"gemm".  `cpu_baseline` times the reference's per-token CPU path (f32 GEMV over
+weights dequantized at load, one thread, restated in oracle/) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "openmini-v1_amd"))
+
+METRIC = "Q4_0 GEMV HBM GB/s (% of peak) at 4096x11008 b=1; Q8_0 GEMM TFLOP/s M=512"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+Q4_0, Q8_0 = 2, 7
+MALL_DEFEAT_BYTES = 1 << 30
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_steps(launch, steps: int, stream, hipr) -> float:
+    """Wall time (ms) of `steps` back-to-back launches between events on `stream`."""
+    hipr.hip().hipDeviceSynchronize()
+    e0, e1 = hipr.Event(), hipr.Event()
+    e0.record(stream)
+    for i in range(steps):
+        launch(i)
+    e1.record(stream)
+    e1.synchronize()
+    hipr.hip().hipDeviceSynchronize()
+    return e0.elapsed_ms(e1)
+
+
+def time_each_launch(launch, steps: int, stream, hipr) -> float:
+    """Average duration (ms) of one launch, from an event pair around each launch."""
+    hipr.hip().hipDeviceSynchronize()
+    evs = [(hipr.Event(), hipr.Event()) for _ in range(steps)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        launch(i)
+        b.record(stream)
+    evs[-1][1].synchronize()
+    hipr.hip().hipDeviceSynchronize()
+    return float(np.mean([a.elapsed_ms(b) for a, b in evs]))
+
+
+def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed=0x5EED0001):
+    from openmini_qmm import synth
+    blocks = synth.weight_blocks(qtype, N, K, seed=seed)
+    wbytes = blocks.size
+    copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
+    log(f"gemv type={qtype} N={N} K={K} B={batch}: {copies} weight copies x {wbytes} B")
+    ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
+    x = synth.normal(seed + 0x8000, (batch, K), 1.0)
+    dx = qmm.DeviceBuffer.from_numpy(x)
+    dy = qmm.DeviceBuffer(batch * N * 4)
+    dy_check = qmm.DeviceBuffer(batch * N * 4)
+    sh = stream.handle
+
+    def launch(i):
+        ws[i % copies].gemv(dx, dy, batch, sh)
+
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    # every copy computes the same y (bitwise: fixed reduction order)
+    ws[0].gemv(dx, dy_check, batch, sh)
+    ws[-1].gemv(dx, dy, batch, sh)
+    stream.synchronize()
+    if not np.array_equal(dy.download(np.float32, (batch, N)), dy_check.download(np.float32, (batch, N))):
+        raise RuntimeError("GEMV copies disagree")
+    total_ms = time_steps(launch, steps, sh, hipr)
+    per_launch_ms = time_each_launch(launch, steps, sh, hipr)
+    alg_bytes = wbytes + batch * K * 4 + batch * N * 4
+    res = {
+        "N": N, "K": K, "batch": batch, "weight_bytes": wbytes, "alg_bytes_per_step": alg_bytes,
+        "weight_copies": copies, "rotated_bytes": copies * wbytes,
+        "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
+        "gbs_wall": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
+        "gbs_kernel": alg_bytes / (per_launch_ms * 1e-3) / 1e9,
+        "blocks": blocks, "x": x,
+    }
+    for w in ws:
+        w.close()
+    return res
+
+
+def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q8_0, seed=0x5EED0003):
+    from openmini_qmm import synth
+    blocks = synth.weight_blocks(qtype, N, K, seed=seed)
+    copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // blocks.size))
+    log(f"gemm type={qtype} N={N} K={K} M={M}: {copies} weight copies")
+    ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
+    xb = synth.to_bf16_bits(synth.normal(seed + 0x8000, (M, K), 1.0))
+    dx = qmm.DeviceBuffer.from_numpy(xb)
+    dy = qmm.DeviceBuffer(M * N * 4)
+    sh = stream.handle
+
+    def launch(i):
+        ws[i % copies].gemm_bf16(dx, dy, M, sh)
+
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    total_ms = time_steps(launch, steps, sh, hipr)
+    per_launch_ms = time_each_launch(launch, steps, sh, hipr)
+    flops = 2.0 * M * N * K
+    for w in ws:
+        w.close()
+    return {
+        "N": N, "K": K, "M": M, "weight_copies": copies,
+        "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
+        "tflops_wall": flops * steps / (total_ms * 1e-3) / 1e12,
+        "tflops_kernel": flops / (per_launch_ms * 1e-3) / 1e12,
+        "flops": flops,
+    }
+
+
+def cpu_baseline(gemv: dict, seconds: float) -> dict:
+    """The reference's per-token CPU path, restated in oracle/ (kind "port"): f32 GEMV
+    over weights dequantized once at load (quant_loader.rs:76-92, model.rs:1050-1064,
+    matrixmultiply single-threaded), timed on this host for ~`seconds`."""
+    from oracle import oracle
+    N, K = gemv["N"], gemv["K"]
+    w = oracle.dequantize(Q4_0, gemv["blocks"], N * K).reshape(N, K)
+    x = gemv["x"]
+    y_ref = oracle.cpu_asrun_linear(w, x, None, False)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.cpu_asrun_linear(w, x, None, False)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per_call = el / reps
+    # all host cores (up to the box's 16-core share) on the quant_simd-style fused path
+    threads = max(1, min(16, os.cpu_count() or 1))
+    y = np.empty((1, N), dtype=np.float32)
+    rows = np.linspace(0, N, threads + 1).astype(int)
+
+    def part(i):
+        oracle.cpu_fused_linear(Q4_0, gemv["blocks"], N, K, x, y, int(rows[i]), int(rows[i + 1]))
+
+    with cf.ThreadPoolExecutor(threads) as ex:
+        list(ex.map(part, range(threads)))
+        reps_f, t0 = 0, time.perf_counter()
+        while True:
+            list(ex.map(part, range(threads)))
+            reps_f += 1
+            el_f = time.perf_counter() - t0
+            if el_f >= seconds / 2:
+                break
+    assert np.max(np.abs(y - y_ref)) <= 1e-3 * np.max(np.abs(y_ref))
+    per_call_f = el_f / reps_f
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    b = gemv["alg_bytes_per_step"]
+    return {
+        "value": round(b / per_call / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"{reps} calls of the f32 GEMV over the dequantized {N}x{K} weight "
+                  f"({el:.1f} s); GB/s counts the same Q4_0 algorithmic bytes as the GPU",
+        "ms_per_call": round(per_call * 1e3, 3),
+        "host": {"cpu_model": model, "nproc": os.cpu_count()},
+        "all_cores_fused": {"value": round(b / per_call_f / 1e9, 3), "unit": "GB/s",
+                            "cores": threads, "ms_per_call": round(per_call_f * 1e3, 3),
+                            "sample": f"{reps_f} calls, quant_simd-style dequant+dot from the "
+                                      f"Q4_0 blocks, {threads} threads"},
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build targets a single MI355X and runs no "
+              f"collectives (asked for --gpus {args.gpus})", file=sys.stderr)
+        return 2
+
+    import openmini_qmm as qmm
+    from openmini_qmm import hip_runtime as hipr
+    qmm.init(0)
+    stream = qmm.Stream()
+    info = qmm.HipQuantOps().device_info()
+    log(info)
+
+    g = bench_gemv(qmm, hipr, stream, args.steps, args.warmup, N=11008, K=4096)
+    log(f"q4_0 gemv 11008x4096: wall {g['gbs_wall']:.1f} GB/s, kernel {g['gbs_kernel']:.1f} GB/s "
+        f"({g['kernel_ms'] * 1e3:.2f} us)")
+    down = bench_gemv(qmm, hipr, stream, args.steps, args.warmup, N=4096, K=11008, seed=0x5EED0002)
+    log(f"q4_0 gemv 4096x11008: wall {down['gbs_wall']:.1f} GB/s, kernel {down['gbs_kernel']:.1f} GB/s")
+    gemm = None
+    if not args.no_gemm:
+        gemm = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
+        log(f"q8_0 gemm M=512: wall {gemm['tflops_wall']:.1f} TFLOP/s, kernel "
+            f"{gemm['tflops_kernel']:.1f} TFLOP/s")
+    cpu = None if args.no_cpu else cpu_baseline(g, args.cpu_seconds)
+
+    achieved = g["gbs_kernel"]
+    out = {
+        "metric": METRIC,
+        "value": round(g["gbs_wall"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "q4_0_gemv_n11008_k4096_b1", "N": g["N"], "K": g["K"], "batch": 1,
+                   "weight": "Q4_0 from N(0, 0.02)", "x": "f32 N(0, 1)",
+                   "weight_copies": g["weight_copies"], "rotated_bytes": g["rotated_bytes"],
+                   "alg_bytes_per_step": g["alg_bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us": round(g["kernel_ms"] * 1e3, 3)},
+        "pct_of_hbm_peak_wall": round(100.0 * g["gbs_wall"] / HBM_PEAK_GBS, 2),
+        "down_proj": {"workload": "q4_0_gemv_n4096_k11008_b1", "value": round(down["gbs_wall"], 2),
+                      "unit": "GB/s", "kernel_gbs": round(down["gbs_kernel"], 2),
+                      "kernel_us": round(down["kernel_ms"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    if gemm:
+        out["gemm"] = {
+            "metric": "Q8_0 GEMM TFLOP/s M=512", "workload": "q8_0_gemm_n11008_k4096_m512_bf16x",
+            "value": round(gemm["tflops_wall"], 2), "unit": "TFLOP/s", "dtype": "bf16",
+            "ms_per_step": round(gemm["ms_per_step"], 6),
+            "roofline": {"bound": "mfma", "achieved": round(gemm["tflops_kernel"], 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel_us": round(gemm["kernel_ms"] * 1e3, 3)},
+        }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,186 @@
+/*
+ * openmini_qmm.h -- C ABI of the MI355X (gfx950) quantized linear layer.
+ *
+ * The GGUF block-quantized matmul (Q4_0 / Q8_0 weight blocks x fp32 / bf16
+ * activations) behind OpenMini-V1's matmul operator.  Rust (or any FFI caller)
+ * binds these symbols; everything under them is hand-written HIP for gfx950.
+ *
+ * Conventions follow openmini-server/native/include/openmini.h:
+ *   - `openmini_` prefix, `#pragma once`, `extern "C"` (openmini.h:1-9);
+ *   - opaque handle typedefs (openmini.h:16-18);
+ *   - status codes whose values coincide with openmini_error_t where the meaning is
+ *     shared (openmini.h:20-31); the CUDA code (-6) is not reused, HIP failures
+ *     report OPENMINI_QMM_ERR_HIP;
+ *   - results through out-pointers (openmini.h:90-94), caller frees through
+ *     openmini_qmm_free_* (openmini.h:96,108,142).
+ * No call aborts: every failure returns a status and leaves a message in the
+ * calling thread's openmini_qmm_last_error().
+ *
+ * Reference paths are relative to openmini-server/ of skin1987/OpenMini-V1.
+ *
+ * Threading: a weight handle is immutable after upload and may be shared by
+ * threads; each call runs on the stream it is given (NULL = the device's null
+ * stream).  Device pointers (d_*) must stay valid until the stream reaches the
+ * call.  Host-pointer calls (no d_ prefix) are synchronous.
+ */
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The library is built with hidden visibility; only these declarations export. */
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+#define OPENMINI_QMM_VERSION_MAJOR 0
+#define OPENMINI_QMM_VERSION_MINOR 1
+#define OPENMINI_QMM_VERSION_PATCH 0
+#define OPENMINI_QMM_VERSION_STRING "0.1.0"
+
+typedef enum {
+    OPENMINI_QMM_OK = 0,
+    OPENMINI_QMM_ERR_MEMORY = -1,        /* = OPENMINI_ERR_MEMORY */
+    OPENMINI_QMM_ERR_INVALID_PARAM = -2, /* = OPENMINI_ERR_INVALID_PARAM */
+    OPENMINI_QMM_ERR_MODEL_LOAD = -3,    /* = OPENMINI_ERR_MODEL_LOAD */
+    OPENMINI_QMM_ERR_INFERENCE = -4,     /* = OPENMINI_ERR_INFERENCE */
+    OPENMINI_QMM_ERR_UNSUPPORTED = -5,   /* = OPENMINI_ERR_UNSUPPORTED: QuantError::UnsupportedType */
+    OPENMINI_QMM_ERR_HIP = -10,          /* HIP runtime failure (no device, launch error, ...) */
+    OPENMINI_QMM_ERR_INSUFFICIENT_DATA = -11 /* QuantError::InsufficientData{expected, actual} */
+} openmini_qmm_status_t;
+
+/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240). */
+typedef enum {
+    OPENMINI_QMM_Q4_0 = 2,
+    OPENMINI_QMM_Q8_0 = 7
+} openmini_qmm_type_t;
+
+/* A quantized weight W[n_rows, k_cols] resident in HBM in the GPU layout. */
+typedef struct openmini_qweight openmini_qweight_t;
+
+typedef struct {
+    int32_t type;            /* openmini_qmm_type_t */
+    int32_t device;          /* HIP device ordinal holding the weight */
+    int64_t n_rows;          /* N: output features */
+    int64_t k_cols;          /* K: input features, a multiple of 32 */
+    int64_t blocks_per_row;  /* K / 32 */
+    size_t gguf_bytes;       /* N * K / 32 * bytes_per_block (GGUF data_size) */
+    size_t device_bytes;     /* HBM held by the handle */
+} openmini_qmm_weight_info_t;
+
+/* ---- library / device ---------------------------------------------------------- */
+
+/* Library version string (cf. openmini_version, openmini.h:87). */
+const char* openmini_qmm_version(void);
+
+/* Selects `device` for this thread and checks it is a gfx950 part
+ * (cf. openmini_init, openmini.h:85).  Idempotent. */
+int openmini_qmm_init(int device);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* openmini_qmm_last_error(void);
+
+/* GpuQuantOps::is_available (src/model/inference/quant_simd.rs:2979): 1 when a
+ * gfx950 device is usable, else 0.  Never fails. */
+int openmini_qmm_is_available(void);
+
+/* GpuQuantOps::device_info (quant_simd.rs:2982): writes a NUL-terminated
+ * description into buf (truncated to buf_len). */
+int openmini_qmm_device_info(char* buf, size_t buf_len);
+
+/* GgufTensor::data_size (src/model/inference/gguf.rs:431-438):
+ * ceil(n_elements / 32) * bytes_per_block.  Pure host computation. */
+int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes);
+
+/* GpuQuantOps::estimate_memory_usage (quant_simd.rs:2985): device bytes a
+ * dequantization of n_elements needs (GGUF input + f32 output). */
+size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
+
+/* ---- weight upload / repack (the loader's layout step) ---------------------------
+ * Replaces dequantize-at-load: QuantizedWeightLoader::load_tensor_data
+ * (src/model/inference/quant_loader.rs:76-92) -> GgufFile::get_tensor_data_by_ref
+ * (gguf.rs:2062-2110) -> quant::dequantize (quant.rs:56).  Takes the tensor's raw
+ * GGUF blocks (row n = k_cols/32 consecutive blocks, ggml ne0 = K), keeps them
+ * quantized and repacks them on the GPU for its access pattern.
+ * Errors: INVALID_PARAM (k_cols % 32, sizes <= 0), UNSUPPORTED (type),
+ * INSUFFICIENT_DATA (gguf_bytes < required). */
+int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes,
+                        int64_t n_rows, int64_t k_cols, openmini_qweight_t** out_weight);
+
+/* Same, from GGUF blocks already in device memory (e.g. copied straight from the
+ * mmap); the repack runs on `stream`, the handle is usable once it completes. */
+int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_bytes,
+                               int64_t n_rows, int64_t k_cols, void* stream,
+                               openmini_qweight_t** out_weight);
+
+void openmini_qmm_free_weight(openmini_qweight_t* weight);
+
+int openmini_qmm_weight_info(const openmini_qweight_t* weight,
+                             openmini_qmm_weight_info_t* info);
+
+/* ---- the operator -----------------------------------------------------------------
+ * linear(x, W) = x . W^T (src/model/inference/model.rs:1050-1064, GemmEngine::matmul
+ * gemm_engine.rs:40), on the quantized W without materialising f32 weights. */
+
+/* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
+ * Any batch >= 1 (HBM-bound up to 8; larger batches run in slices of 8 rows).
+ * d_x must be 16-byte aligned. */
+int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
+                      int64_t batch, void* stream);
+
+/* Prefill GEMM: y[m, N] = x[m, K] . W^T with bf16 activations (raw bf16 bits),
+ * fp32 output, on bf16 MFMA with exact integer codes and fp32 per-block scales.
+ * d_x must be 16-byte aligned. */
+int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
+                           int64_t m, void* stream);
+
+/* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
+ * fp32 in/out, synchronous.  Uses the GEMV kernels (exact fp32 activations). */
+int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,
+                             int64_t m);
+
+/* ---- dequantization (GpuQuantOps, src/model/inference/quant_simd.rs:2944-2986) ----- */
+
+/* Dequantizes an uploaded weight to f32 W[N, K] (row-major) in device memory.
+ * Bit-identical to quant::dequantize of the original GGUF bytes. */
+int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, void* stream);
+
+/* quant_simd::safe_dequantize semantics (quant_simd.rs:150-241, 284-302) on raw
+ * GGUF bytes in device memory: n == 0 -> OK (nothing written); gguf_bytes <
+ * ceil(n/32)*bpb -> INSUFFICIENT_DATA with *expected_bytes set; other types ->
+ * UNSUPPORTED.  Writes n floats. expected_bytes may be NULL. */
+int openmini_qmm_dequantize_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n,
+                                   float* d_out, void* stream, size_t* expected_bytes);
+
+/* GpuQuantOps::dequantize_{q4_0,q8_0}_gpu(&[u8], n) -> Vec<f32> (quant_simd.rs:2955-2958):
+ * host bytes in, host floats out, synchronous, same validation as above. */
+int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_t n,
+                            float* out, size_t* expected_bytes);
+
+/* ---- device memory and streams for callers without a HIP binding of their own ----- */
+
+int openmini_qmm_malloc(void** d_ptr, size_t bytes);
+int openmini_qmm_free(void* d_ptr);
+int openmini_qmm_memcpy_h2d(void* d_dst, const void* src, size_t bytes, void* stream);
+int openmini_qmm_memcpy_d2h(void* dst, const void* d_src, size_t bytes, void* stream);
+int openmini_qmm_memset(void* d_dst, int value, size_t bytes, void* stream);
+int openmini_qmm_stream_create(void** out_stream);
+int openmini_qmm_stream_destroy(void* stream);
+int openmini_qmm_stream_synchronize(void* stream);
+
+/* Bandwidth calibration: a plain streaming copy kernel of `bytes` (multiple of 16,
+ * 16-byte aligned pointers) on `stream`; the yardstick that HBM traffic counters
+ * of the GEMV are scaled against.  No counterpart in the reference. */
+int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void* stream);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif

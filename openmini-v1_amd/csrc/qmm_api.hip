@@ -1,0 +1,465 @@
+// C-ABI of libopenmini_qmm.so (declarations and reference citations in
+// include/openmini_qmm.h).  Host code only: validation, device selection, memory
+// management and kernel dispatch.  Every failure returns a status and records a
+// message for openmini_qmm_last_error(); nothing aborts.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "qmm_internal.hpp"
+
+struct openmini_qweight {
+    qmm::Weight w;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return OPENMINI_QMM_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(OPENMINI_QMM_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(expr, what)                         \
+    do {                                            \
+        hipError_t e_ = (expr);                     \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+bool type_supported(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
+
+// Device probing is done once per device; the result is cached.
+std::mutex g_dev_mu;
+int g_dev_state[64];  // 0 unknown, 1 gfx950, -1 unusable
+
+int ensure_device(int* out_dev) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(OPENMINI_QMM_ERR_HIP, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_dev_state[dev] == 0) {
+        hipDeviceProp_t p;
+        e = hipGetDeviceProperties(&p, dev);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+        g_dev_state[dev] = (std::strncmp(p.gcnArchName, "gfx950", 6) == 0) ? 1 : -1;
+        if (g_dev_state[dev] < 0)
+            return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950",
+                        dev, p.gcnArchName);
+    }
+    if (g_dev_state[dev] < 0)
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "device %d is not a gfx950 part", dev);
+    if (out_dev) *out_dev = dev;
+    return OPENMINI_QMM_OK;
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_cols) {
+    if (!type_supported(type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d (Q4_0=2, Q8_0=7)", type);
+    if (n_rows <= 0 || k_cols <= 0)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "invalid shape [%lld, %lld]", (long long)n_rows,
+                    (long long)k_cols);
+    if (k_cols % qmm::kQK != 0)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "k_cols=%lld is not a multiple of 32",
+                    (long long)k_cols);
+    if (n_rows > INT32_MAX || k_cols / qmm::kQK > INT32_MAX / 64)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld] too large", (long long)n_rows,
+                    (long long)k_cols);
+    const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
+    if (gguf_bytes < need)
+        return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA,
+                    "InsufficientData: expected %zu bytes, actual %zu", need, gguf_bytes);
+    return OPENMINI_QMM_OK;
+}
+
+int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qweight** out) {
+    openmini_qweight* h = new (std::nothrow) openmini_qweight();
+    if (!h) return fail(OPENMINI_QMM_ERR_MEMORY, "host allocation failed");
+    qmm::Weight& w = h->w;
+    w.type = type;
+    w.device = dev;
+    w.n = n_rows;
+    w.k = k_cols;
+    w.nb = k_cols / qmm::kQK;
+    const size_t nblocks = (size_t)w.n * (size_t)w.nb;
+    const size_t code_bytes = round_up(nblocks * qmm::code_bytes_per_block(type), 256);
+    const size_t scale_bytes = round_up(nblocks * 2, 256);
+    w.device_bytes = code_bytes + scale_bytes;
+    hipError_t e = hipMalloc(&w.base, w.device_bytes);
+    if (e != hipSuccess) {
+        delete h;
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) for weight failed: %s", w.device_bytes,
+                    hipGetErrorString(e));
+    }
+    w.codes = static_cast<uint8_t*>(w.base);
+    w.scales = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(w.base) + code_bytes);
+    *out = h;
+    return OPENMINI_QMM_OK;
+}
+
+int check_weight(const openmini_qweight* h) {
+    if (!h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null weight handle");
+    int dev = 0;
+    int rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (dev != h->w.device)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "weight lives on device %d, current device is %d",
+                    h->w.device, dev);
+    return OPENMINI_QMM_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char* openmini_qmm_version(void) { return OPENMINI_QMM_VERSION_STRING; }
+
+const char* openmini_qmm_last_error(void) { return g_last_error.c_str(); }
+
+int openmini_qmm_init(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) return fail(OPENMINI_QMM_ERR_HIP, "no HIP device available");
+    if (device < 0 || device >= count)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "device %d out of range (count %d)", device, count);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    return ok();
+}
+
+int openmini_qmm_is_available(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return 0;
+    std::string saved = g_last_error;
+    const int rc = ensure_device(nullptr);
+    g_last_error = saved;
+    return rc == OPENMINI_QMM_OK ? 1 : 0;
+}
+
+int openmini_qmm_device_info(char* buf, size_t buf_len) {
+    if (!buf || buf_len == 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null buffer");
+    int dev = 0;
+    int rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) {
+        std::snprintf(buf, buf_len, "HipQuantOps { device: unavailable }");
+        return rc;
+    }
+    hipDeviceProp_t p;
+    HIP_TRY(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+    std::snprintf(buf, buf_len, "HipQuantOps { device: %d, name: %s, arch: %s, cus: %d, hbm_bytes: %zu }",
+                  dev, p.name, p.gcnArchName, p.multiProcessorCount, (size_t)p.totalGlobalMem);
+    return ok();
+}
+
+int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes) {
+    if (!out_bytes) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_bytes");
+    if (!type_supported(type)) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
+    *out_bytes = (n_elements + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    return ok();
+}
+
+size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements) {
+    const size_t bpb = type_supported(type) ? (size_t)qmm::bytes_per_block(type) : 4u * qmm::kQK;
+    return (n_elements + qmm::kQK - 1) / qmm::kQK * bpb + n_elements * sizeof(float);
+}
+
+int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes, int64_t n_rows,
+                        int64_t k_cols, openmini_qweight_t** out_weight) {
+    if (!out_weight) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_weight");
+    *out_weight = nullptr;
+    int rc = validate_weight_args(type, gguf_bytes, n_rows, k_cols);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!gguf_blocks) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null gguf_blocks");
+    int dev = 0;
+    rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, need);
+    if (e != hipSuccess)
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) staging failed: %s", need, hipGetErrorString(e));
+    openmini_qweight* h = nullptr;
+    rc = alloc_weight(type, n_rows, k_cols, dev, &h);
+    if (rc != OPENMINI_QMM_OK) {
+        (void)hipFree(staging);
+        return rc;
+    }
+    e = hipMemcpy(staging, gguf_blocks, need, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = qmm::launch_repack(type, static_cast<const uint8_t*>(staging), n_rows * (k_cols / qmm::kQK),
+                               h->w.codes, h->w.scales, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    (void)hipFree(staging);
+    if (e != hipSuccess) {
+        openmini_qmm_free_weight(h);
+        return hip_fail(e, "upload/repack");
+    }
+    *out_weight = h;
+    return ok();
+}
+
+int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_bytes, int64_t n_rows,
+                               int64_t k_cols, void* stream, openmini_qweight_t** out_weight) {
+    if (!out_weight) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_weight");
+    *out_weight = nullptr;
+    int rc = validate_weight_args(type, gguf_bytes, n_rows, k_cols);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_gguf_blocks) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null d_gguf_blocks");
+    int dev = 0;
+    rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    openmini_qweight* h = nullptr;
+    rc = alloc_weight(type, n_rows, k_cols, dev, &h);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipError_t e = qmm::launch_repack(type, static_cast<const uint8_t*>(d_gguf_blocks),
+                                      n_rows * (k_cols / qmm::kQK), h->w.codes, h->w.scales,
+                                      as_stream(stream));
+    if (e != hipSuccess) {
+        openmini_qmm_free_weight(h);
+        return hip_fail(e, "repack launch");
+    }
+    *out_weight = h;
+    return ok();
+}
+
+void openmini_qmm_free_weight(openmini_qweight_t* weight) {
+    if (!weight) return;
+    if (weight->w.base) {
+        int cur = 0;
+        const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != weight->w.device;
+        if (switch_dev) (void)hipSetDevice(weight->w.device);
+        (void)hipFree(weight->w.base);
+        if (switch_dev) (void)hipSetDevice(cur);
+    }
+    delete weight;
+}
+
+int openmini_qmm_weight_info(const openmini_qweight_t* weight, openmini_qmm_weight_info_t* info) {
+    if (!weight || !info) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null argument");
+    const qmm::Weight& w = weight->w;
+    info->type = w.type;
+    info->device = w.device;
+    info->n_rows = w.n;
+    info->k_cols = w.k;
+    info->blocks_per_row = w.nb;
+    info->gguf_bytes = (size_t)w.n * (size_t)w.nb * qmm::bytes_per_block(w.type);
+    info->device_bytes = w.device_bytes;
+    return ok();
+}
+
+int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t batch,
+                      void* stream) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
+    if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    const qmm::Weight& w = weight->w;
+    for (int64_t b0 = 0; b0 < batch; b0 += 8) {
+        const int nb = (int)((batch - b0) < 8 ? (batch - b0) : 8);
+        hipError_t e = qmm::launch_gemv(w, d_x + b0 * w.k, d_y + b0 * w.n, nb, as_stream(stream));
+        if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    }
+    return ok();
+}
+
+int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y, int64_t m,
+                           void* stream) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
+    if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    hipError_t e = qmm::launch_gemm_bf16(weight->w, d_x, d_y, m, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemm launch");
+    return ok();
+}
+
+int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y, int64_t m) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!x || !y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
+    if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
+    const qmm::Weight& w = weight->w;
+    const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
+    void *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipMalloc(&dx, xb);
+    if (e == hipSuccess) e = hipMalloc(&dy, yb);
+    if (e != hipSuccess) {
+        (void)hipFree(dx);
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
+    }
+    e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
+    for (int64_t b0 = 0; e == hipSuccess && b0 < m; b0 += 8) {
+        const int nb = (int)((m - b0) < 8 ? (m - b0) : 8);
+        e = qmm::launch_gemv(w, static_cast<const float*>(dx) + b0 * w.k, static_cast<float*>(dy) + b0 * w.n,
+                             nb, nullptr);
+    }
+    if (e == hipSuccess) e = hipMemcpy(y, dy, yb, hipMemcpyDeviceToHost);
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    if (e != hipSuccess) return hip_fail(e, "linear_host");
+    return ok();
+}
+
+int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, void* stream) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out");
+    if (!aligned16(d_out)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "out must be 16-byte aligned");
+    hipError_t e = qmm::launch_dequant_weight(weight->w, d_out, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return ok();
+}
+
+static int validate_dequant(int type, size_t gguf_bytes, size_t n, size_t* expected_bytes) {
+    if (expected_bytes) *expected_bytes = 0;
+    if (!type_supported(type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "UnsupportedType(%d)", type);
+    const size_t need = (n + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    if (gguf_bytes < need) {
+        if (expected_bytes) *expected_bytes = need;
+        return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA, "InsufficientData: expected %zu bytes, actual %zu",
+                    need, gguf_bytes);
+    }
+    return OPENMINI_QMM_OK;
+}
+
+int openmini_qmm_dequantize_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n, float* d_out,
+                                   void* stream, size_t* expected_bytes) {
+    int rc = validate_dequant(type, gguf_bytes, n, expected_bytes);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (n == 0) return ok();
+    if (!d_gguf || !d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipError_t e = qmm::launch_dequant_gguf(type, static_cast<const uint8_t*>(d_gguf), n, d_out,
+                                            as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return ok();
+}
+
+int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out,
+                            size_t* expected_bytes) {
+    int rc = validate_dequant(type, gguf_bytes, n, expected_bytes);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (n == 0) return ok();
+    if (!gguf || !out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t need = (n + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    void *din = nullptr, *dout = nullptr;
+    hipError_t e = hipMalloc(&din, need);
+    if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipFree(din);
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for dequantize failed: %s", hipGetErrorString(e));
+    }
+    e = hipMemcpy(din, gguf, need, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = qmm::launch_dequant_gguf(type, static_cast<const uint8_t*>(din), n, static_cast<float*>(dout),
+                                     nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(din);
+    (void)hipFree(dout);
+    if (e != hipSuccess) return hip_fail(e, "dequantize");
+    return ok();
+}
+
+int openmini_qmm_malloc(void** d_ptr, size_t bytes) {
+    if (!d_ptr) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null d_ptr");
+    *d_ptr = nullptr;
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipError_t e = hipMalloc(d_ptr, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return ok();
+}
+
+int openmini_qmm_free(void* d_ptr) {
+    if (!d_ptr) return ok();
+    HIP_TRY(hipFree(d_ptr), "hipFree");
+    return ok();
+}
+
+int openmini_qmm_memcpy_h2d(void* d_dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!d_dst || !src) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    HIP_TRY(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)), "hipMemcpyAsync H2D");
+    HIP_TRY(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    return ok();
+}
+
+int openmini_qmm_memcpy_d2h(void* dst, const void* d_src, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!dst || !d_src) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, as_stream(stream)), "hipMemcpyAsync D2H");
+    HIP_TRY(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    return ok();
+}
+
+int openmini_qmm_memset(void* d_dst, int value, size_t bytes, void* stream) {
+    if (bytes == 0) return ok();
+    if (!d_dst) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    HIP_TRY(hipMemsetAsync(d_dst, value, bytes, as_stream(stream)), "hipMemsetAsync");
+    return ok();
+}
+
+int openmini_qmm_stream_create(void** out_stream) {
+    if (!out_stream) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_stream");
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipStream_t s = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *out_stream = s;
+    return ok();
+}
+
+int openmini_qmm_stream_destroy(void* stream) {
+    if (!stream) return ok();
+    HIP_TRY(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+    return ok();
+}
+
+int openmini_qmm_stream_synchronize(void* stream) {
+    HIP_TRY(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    return ok();
+}
+
+int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void* stream) {
+    if (!d_dst || !d_src) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    if (bytes % 16 || !aligned16(d_dst) || !aligned16(d_src))
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "stream_copy needs 16-byte sizes and alignment");
+    hipError_t e = qmm::launch_stream_copy(d_dst, d_src, bytes, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "stream_copy launch");
+    return ok();
+}
+
+}  // extern "C"

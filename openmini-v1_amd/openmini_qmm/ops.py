@@ -1,0 +1,312 @@
+"""Host-side mirror of OpenMini-V1's quantized-linear operator interface, over the
+HIP C-ABI.  Names, argument meaning and error behaviour follow the reference
+(paths relative to openmini-server/):
+
+  QuantError / InsufficientData / UnsupportedType   quant_simd.rs:91-103
+  safe_dequantize{,_q4_0,_q8_0}                     quant_simd.rs:150-241, 284-302
+  GpuQuantOps -> HipQuantOps                        quant_simd.rs:2944-2986 (trait),
+                                                    :3137-3188 (the CUDA stub it replaces)
+  GemmEngine -> HipQuantGemmEngine                  model/inference/gemm_engine.rs:37-56
+  linear / linear_gemm                              model/inference/model.rs:1050-1064
+
+Every computation runs in libopenmini_qmm.so on the GPU; nothing here falls back
+to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+
+import numpy as np
+
+from . import _native
+from ._native import QmmError, check, lib
+
+QK = 32
+
+
+class GgufTensorType(enum.IntEnum):
+    """GGUF type ids, model/inference/gguf.rs:219-240 (the subset this path handles,
+    plus F32/F16 so callers can ask for them and get UnsupportedType)."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q8_0 = 7
+
+    def bytes_per_block(self) -> int:  # gguf.rs:356-379
+        return {0: 4, 1: 2, 2: 18, 7: 34}[int(self)]
+
+    def block_size(self) -> int:  # gguf.rs:327-338
+        return {0: 1, 1: 1, 2: 32, 7: 32}[int(self)]
+
+
+# ---- quant_simd::QuantError --------------------------------------------------------
+
+class QuantError(Exception):
+    pass
+
+
+class InsufficientData(QuantError):
+    def __init__(self, expected: int, actual: int):
+        super().__init__(f"InsufficientData {{ expected: {expected}, actual: {actual} }}")
+        self.expected = expected
+        self.actual = actual
+
+
+class UnsupportedType(QuantError):
+    def __init__(self, tensor_type):
+        super().__init__(f"UnsupportedType({tensor_type!r})")
+        self.tensor_type = tensor_type
+
+
+class InvalidInput(QuantError):
+    pass
+
+
+def _as_u8(data) -> np.ndarray:
+    if isinstance(data, np.ndarray):
+        return np.ascontiguousarray(data.view(np.uint8).ravel())
+    return np.frombuffer(bytes(data), dtype=np.uint8)
+
+
+def _ptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data) if a.size else None
+
+
+# ---- device memory ----------------------------------------------------------------
+
+class DeviceBuffer:
+    """Owned device allocation (openmini_qmm_malloc / openmini_qmm_free)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = ctypes.c_void_p()
+        check(lib().openmini_qmm_malloc(ctypes.byref(self.ptr), self.nbytes))
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray, stream=None) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().openmini_qmm_memcpy_h2d(self.ptr, _ptr(a), a.nbytes, stream))
+
+    def download(self, dtype, shape, stream=None) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(lib().openmini_qmm_memcpy_d2h(_ptr(out), self.ptr, out.nbytes, stream))
+        return out
+
+    def fill(self, byte: int, stream=None) -> None:
+        check(lib().openmini_qmm_memset(self.ptr, byte, self.nbytes, stream))
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().openmini_qmm_free(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        self.handle = ctypes.c_void_p()
+        check(lib().openmini_qmm_stream_create(ctypes.byref(self.handle)))
+
+    def synchronize(self) -> None:
+        check(lib().openmini_qmm_stream_synchronize(self.handle))
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().openmini_qmm_stream_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def init(device: int = 0) -> None:
+    check(lib().openmini_qmm_init(device))
+
+
+# ---- weights ------------------------------------------------------------------------
+
+class QuantizedWeight:
+    """A GGUF Q4_0/Q8_0 tensor W[n_rows, k_cols] uploaded and repacked in HBM.
+
+    Replaces QuantizedWeightLoader::load_tensor_data (quant_loader.rs:76-92), which
+    dequantizes to f32 at load; here the raw blocks stay quantized on the GPU."""
+
+    def __init__(self, tensor_type: int, gguf_blocks, n_rows: int, k_cols: int):
+        data = _as_u8(gguf_blocks)
+        self.handle = ctypes.c_void_p()
+        check(lib().openmini_qmm_upload(int(tensor_type), _ptr(data), data.size, int(n_rows),
+                                        int(k_cols), ctypes.byref(self.handle)))
+        self.tensor_type = GgufTensorType(int(tensor_type))
+        self.n_rows = int(n_rows)
+        self.k_cols = int(k_cols)
+
+    @classmethod
+    def from_device(cls, tensor_type: int, d_blocks: DeviceBuffer, nbytes: int, n_rows: int,
+                    k_cols: int, stream=None) -> "QuantizedWeight":
+        self = cls.__new__(cls)
+        self.handle = ctypes.c_void_p()
+        check(lib().openmini_qmm_upload_device(int(tensor_type), d_blocks.ptr, int(nbytes),
+                                               int(n_rows), int(k_cols), stream,
+                                               ctypes.byref(self.handle)))
+        self.tensor_type = GgufTensorType(int(tensor_type))
+        self.n_rows, self.k_cols = int(n_rows), int(k_cols)
+        return self
+
+    def info(self) -> _native.WeightInfo:
+        info = _native.WeightInfo()
+        check(lib().openmini_qmm_weight_info(self.handle, ctypes.byref(info)))
+        return info
+
+    def dequantize(self) -> np.ndarray:
+        """f32 W[n_rows, k_cols], bit-identical to quant::dequantize of the blocks."""
+        out = DeviceBuffer(self.n_rows * self.k_cols * 4)
+        check(lib().openmini_qmm_dequant_weight(self.handle, out.ptr, None))
+        return out.download(np.float32, (self.n_rows, self.k_cols))
+
+    def gemv(self, d_x: DeviceBuffer, d_y: DeviceBuffer, batch: int, stream=None) -> None:
+        check(lib().openmini_qmm_gemv(self.handle, d_x.ptr, d_y.ptr, int(batch), stream))
+
+    def gemm_bf16(self, d_x: DeviceBuffer, d_y: DeviceBuffer, m: int, stream=None) -> None:
+        check(lib().openmini_qmm_gemm_bf16(self.handle, d_x.ptr, d_y.ptr, int(m), stream))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().openmini_qmm_free_weight(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- quant_simd safe API (validated dequantization) on the GPU ----------------------
+
+def safe_dequantize(data, tensor_type, n: int) -> np.ndarray:
+    """quant_simd::safe_dequantize (quant_simd.rs:284-302): n == 0 -> empty;
+    short input -> InsufficientData{expected, actual}; other types -> UnsupportedType."""
+    tt = int(tensor_type)
+    if tt not in (GgufTensorType.Q4_0, GgufTensorType.Q8_0):
+        raise UnsupportedType(tensor_type)
+    buf = _as_u8(data)
+    out = np.empty(max(int(n), 0), dtype=np.float32)
+    expected = ctypes.c_size_t(0)
+    rc = lib().openmini_qmm_dequantize(tt, _ptr(buf), buf.size, int(n),
+                                       _ptr(out) if n else None, ctypes.byref(expected))
+    if rc == _native.ERR_INSUFFICIENT_DATA:
+        raise InsufficientData(expected.value, buf.size)
+    if rc == _native.ERR_UNSUPPORTED:
+        raise UnsupportedType(tensor_type)
+    check(rc)
+    return out
+
+
+def safe_dequantize_q4_0(data, n: int) -> np.ndarray:
+    return safe_dequantize(data, GgufTensorType.Q4_0, n)
+
+
+def safe_dequantize_q8_0(data, n: int) -> np.ndarray:
+    return safe_dequantize(data, GgufTensorType.Q8_0, n)
+
+
+# ---- GpuQuantOps ----------------------------------------------------------------------
+
+class HipQuantOps:
+    """HIP implementation of trait GpuQuantOps (quant_simd.rs:2944-2986), in place of
+    the CudaQuantOps stub (:3137-3188).  Rust's Result<Vec<f32>, String> maps to a
+    returned array or a raised GpuQuantOpsError carrying the string."""
+
+    class GpuQuantOpsError(RuntimeError):
+        pass
+
+    def _deq(self, tensor_type: int, data, n: int) -> np.ndarray:
+        try:
+            return safe_dequantize(data, tensor_type, n)
+        except (QuantError, QmmError) as e:
+            raise HipQuantOps.GpuQuantOpsError(str(e)) from e
+
+    def dequantize_q4_0_gpu(self, data, n: int) -> np.ndarray:
+        return self._deq(GgufTensorType.Q4_0, data, n)
+
+    def dequantize_q8_0_gpu(self, data, n: int) -> np.ndarray:
+        return self._deq(GgufTensorType.Q8_0, data, n)
+
+    def dequantize_q4_1_gpu(self, data, n: int) -> np.ndarray:
+        raise HipQuantOps.GpuQuantOpsError("Q4_1 is not implemented by the HIP backend")
+
+    def batch_dequantize_gpu(self, tensors) -> list:
+        return [self._deq(t, d, n) for (t, d, n) in tensors]
+
+    def is_available(self) -> bool:
+        return bool(lib().openmini_qmm_is_available())
+
+    def device_info(self) -> str:
+        buf = ctypes.create_string_buffer(512)
+        lib().openmini_qmm_device_info(buf, len(buf))
+        return buf.value.decode()
+
+    def estimate_memory_usage(self, total_elements: int) -> int:
+        return int(lib().openmini_qmm_estimate_memory_usage(int(GgufTensorType.Q4_0),
+                                                            int(total_elements)))
+
+
+# ---- GemmEngine sibling ------------------------------------------------------------------
+
+class HipQuantGemmEngine:
+    """Quantized sibling of trait GemmEngine (gemm_engine.rs:37-56): same shape of API
+    (name, backend_type, matmul, is_available), host arrays at the edge, the weight a
+    device handle created at load.  matmul(x, W) computes x . W^T for W[N, K], i.e.
+    what linear() feeds GemmEngine::matmul after its W.t() copy (model.rs:1050-1064)."""
+
+    def name(self) -> str:
+        return "hip_quant"
+
+    def backend_type(self) -> str:
+        return "HipQuant"
+
+    def is_available(self) -> bool:
+        return bool(lib().openmini_qmm_is_available())
+
+    def matmul(self, x: np.ndarray, weight: QuantizedWeight) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != weight.k_cols:
+            raise InvalidInput(f"x shape {x.shape} does not match W[{weight.n_rows}, {weight.k_cols}]")
+        y = np.empty((x.shape[0], weight.n_rows), dtype=np.float32)
+        check(lib().openmini_qmm_linear_host(weight.handle, _ptr(x), _ptr(y), x.shape[0]))
+        return y
+
+
+_ENGINE = None
+
+
+def get_gemm_engine() -> HipQuantGemmEngine:
+    """Process-wide engine, like get_gemm_engine_manager() (gemm_engine.rs:471-475)."""
+    global _ENGINE
+    if _ENGINE is None:
+        _ENGINE = HipQuantGemmEngine()
+    return _ENGINE
+
+
+def linear_gemm(x: np.ndarray, weight: QuantizedWeight) -> np.ndarray:
+    """model.rs:1060-1064: x . W^T through the engine; errors propagate."""
+    return get_gemm_engine().matmul(x, weight)
+
+
+def linear(x: np.ndarray, weight: QuantizedWeight) -> np.ndarray:
+    """model.rs:1050-1057.  The reference falls back to a CPU dot on engine error;
+    this path has no CPU fallback, so the error propagates."""
+    return get_gemm_engine().matmul(x, weight)

@@ -1,0 +1,81 @@
+"""Synthetic inputs for the benchmark configurations (seeded numpy), quantized to
+GGUF Q4_0 / Q8_0 blocks in the reference's byte layout.
+
+The quantizers are ggml's textbook ones (the reference has no GGUF quantizer; the
+benchmark configurations name them):
+  Q4_0: max = signed value of largest |x| (first on ties); d = max / -8;
+        id = 1/d (0 if d == 0); q = min(15, trunc(x*id + 8.5)); scale = fp16(d)
+  Q8_0: d = amax / 127; id = 1/d (0 if d == 0); q = round_half_away(x*id)
+Q4_0 codes are packed in the reference nibble order: element 2j in the high nibble
+of byte j (openmini-server/src/model/inference/quant.rs:179-188).
+All arithmetic is float32 with separate multiply and add, like the C oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QK = 32
+Q4_0, Q8_0 = 2, 7
+
+
+def normal(seed: int, shape, sigma: float) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(sigma)).astype(np.float32)
+
+
+def quantize_q4_0(x: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, QK)
+    a = np.abs(v)
+    idx = np.argmax(a, axis=1)
+    mx = v[np.arange(v.shape[0]), idx]
+    mx = np.where(a[np.arange(v.shape[0]), idx] == 0, np.float32(0.0), mx).astype(np.float32)
+    d = (mx / np.float32(-8.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    t = (v * inv[:, None]).astype(np.float32) + np.float32(8.5)
+    q = np.minimum(t.astype(np.int8).astype(np.int32), 15).astype(np.uint8)
+    out = np.empty((v.shape[0], 18), dtype=np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = (q[:, 0::2] << 4) | q[:, 1::2]
+    return out.ravel()
+
+
+def _round_half_away(t: np.ndarray) -> np.ndarray:
+    r = np.trunc(t)
+    frac = t - r
+    return r + np.where(np.abs(frac) >= np.float32(0.5), np.sign(t), np.float32(0.0))
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, QK)
+    amax = np.max(np.abs(v), axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    t = (v * inv[:, None]).astype(np.float32)
+    q = _round_half_away(t).astype(np.int8)
+    out = np.empty((v.shape[0], 34), dtype=np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.ravel()
+
+
+def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
+    return quantize_q4_0(x) if qtype == Q4_0 else quantize_q8_0(x)
+
+
+def to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bits, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + np.uint32(0x7FFF) + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def weight_blocks(qtype: int, n_rows: int, k_cols: int, seed: int, sigma: float = 0.02) -> np.ndarray:
+    """GGUF blocks of W[n_rows, k_cols] ~ N(0, sigma), row-major (row n = K/32 blocks)."""
+    return quantize(qtype, normal(seed, (n_rows, k_cols), sigma))

@@ -1,0 +1,72 @@
+"""The C-ABI library loads and exports every symbol include/openmini_qmm.h declares.
+Only host-side validation is exercised here (no device is touched)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "openmini_qmm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(openmini_qmm_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("openmini_qmm_upload", "openmini_qmm_gemv", "openmini_qmm_gemm_bf16",
+                 "openmini_qmm_dequantize", "openmini_qmm_dequant_weight", "openmini_qmm_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from openmini_qmm import _native
+    L = _native.lib()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, missing
+    # the ctypes table covers the header exactly
+    assert sorted(_native.SIGNATURES) == declared_functions()
+
+
+def test_host_only_validation():
+    from openmini_qmm import _native
+    L = _native.lib()
+    assert L.openmini_qmm_version() == b"0.1.0"
+    out = ctypes.c_size_t()
+    assert L.openmini_qmm_required_bytes(2, 4096 * 11008, ctypes.byref(out)) == 0
+    assert out.value == 25_362_432
+    assert L.openmini_qmm_required_bytes(7, 33, ctypes.byref(out)) == 0 and out.value == 68
+    assert L.openmini_qmm_required_bytes(10, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
+    assert L.openmini_qmm_estimate_memory_usage(2, 64) == 36 + 256
+
+    h = ctypes.c_void_p()
+    buf = np.zeros(64, dtype=np.uint8)
+    p = ctypes.c_void_p(buf.ctypes.data)
+    # K not a multiple of 32
+    assert L.openmini_qmm_upload(2, p, buf.size, 1, 48, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
+    assert b"multiple of 32" in L.openmini_qmm_last_error()
+    # too few bytes: InsufficientData{expected=36, actual=20}
+    assert L.openmini_qmm_upload(2, p, 20, 1, 64, ctypes.byref(h)) == _native.ERR_INSUFFICIENT_DATA
+    assert b"expected 36" in L.openmini_qmm_last_error() and b"actual 20" in L.openmini_qmm_last_error()
+    assert L.openmini_qmm_upload(3, p, 64, 1, 32, ctypes.byref(h)) == _native.ERR_UNSUPPORTED
+    # safe_dequantize semantics: n == 0 is Ok, short input reports expected bytes
+    exp = ctypes.c_size_t(123)
+    assert L.openmini_qmm_dequantize(2, None, 0, 0, None, ctypes.byref(exp)) == 0 and exp.value == 0
+    assert L.openmini_qmm_dequantize(2, p, 10, 32, p, ctypes.byref(exp)) == _native.ERR_INSUFFICIENT_DATA
+    assert exp.value == 18
+    assert L.openmini_qmm_dequantize(10, p, 64, 32, p, ctypes.byref(exp)) == _native.ERR_UNSUPPORTED
+
+
+def test_python_mirror_raises_reference_errors():
+    import pytest
+    from openmini_qmm import InsufficientData, UnsupportedType, safe_dequantize_q4_0, safe_dequantize
+    with pytest.raises(InsufficientData) as ei:
+        safe_dequantize_q4_0(bytes(10), 32)
+    assert (ei.value.expected, ei.value.actual) == (18, 10)
+    with pytest.raises(UnsupportedType):
+        safe_dequantize(b"", 10, 32)
+    assert safe_dequantize_q4_0(b"", 0).size == 0

@@ -1,0 +1,114 @@
+"""Decode GEMV on the GPU against the fp64 oracle (model.rs:1050-1064 semantics:
+y = x . W^T), tolerance from tests/parity.py (1e-3 normwise and elementwise)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from openmini_qmm import synth
+from parity import TOL, assert_parity
+
+pytestmark = pytest.mark.gpu
+Q4_0, Q8_0 = 2, 7
+
+
+def run_gemv(qmm, w, x):
+    B, K = x.shape
+    dx = qmm.DeviceBuffer.from_numpy(x)
+    dy = qmm.DeviceBuffer(B * w.n_rows * 4)
+    w.gemv(dx, dy, B)
+    return dy.download(np.float32, (B, w.n_rows))
+
+
+def case(qmm, orc, qtype, N, K, B, seed, sigma=0.02):
+    print(f"gemv type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.weight_blocks(qtype, N, K, seed=seed, sigma=sigma)
+    x = synth.normal(seed + 1, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y = run_gemv(qmm, w, x)
+    ref = orc.linear_f64(qtype, blocks, N, K, x)
+    return assert_parity(y, ref, TOL, f"type={qtype} N={N} K={K} B={B}"), w, blocks, x, y
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("N,K", [(1, 32), (5, 64), (37, 96), (130, 2080), (257, 4128), (64, 8192)])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 8])
+def test_gemv_small_shapes(qmm, orc, qtype, N, K, B):
+    case(qmm, orc, qtype, N, K, B, seed=1000 + N + K + B)
+
+
+@pytest.mark.parametrize("qtype,N,K,B", [
+    (Q4_0, 4096, 4096, 1),      # config 0
+    (Q4_0, 11008, 4096, 1),     # headline, gate/up orientation
+    (Q4_0, 4096, 11008, 1),     # headline, down orientation
+    (Q8_0, 11008, 4096, 1),     # config 1
+    (Q8_0, 4096, 11008, 1),
+    (Q8_0, 11008, 4096, 8),
+    (Q8_0, 4096, 11008, 8),
+])
+def test_gemv_baseline_configs(qmm, orc, qtype, N, K, B):
+    p, *_ = case(qmm, orc, qtype, N, K, B, seed=0x5EED0000 + N + B)
+    print(p)
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_gemv_70b_q_proj(qmm, orc, B):
+    case(qmm, orc, Q4_0, 8192, 8192, B, seed=0x7000 + B, sigma=0.015)
+
+
+def test_gemv_batch_over_8_is_sliced(qmm, orc):
+    p, *_ = case(qmm, orc, Q4_0, 300, 512, 19, seed=5)
+
+
+def test_gemv_linearity_full_size(qmm):
+    """Size-independent property at the largest 70B shape: y(a x1 + x2) = a y(x1) + y(x2)
+    within fp32 reassociation, and y(0) = 0 exactly."""
+    N, K = 28672, 8192
+    print(f"gemv linearity N={N} K={K}", flush=True)
+    blocks = synth.weight_blocks(Q4_0, N, K, seed=77, sigma=0.015)
+    w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
+    x1 = synth.normal(78, (1, K), 1.0)
+    x2 = synth.normal(79, (1, K), 1.0)
+    y1, y2 = run_gemv(qmm, w, x1), run_gemv(qmm, w, x2)
+    y12 = run_gemv(qmm, w, (np.float32(2.0) * x1 + x2).astype(np.float32))
+    assert_parity(y12, 2.0 * y1.astype(np.float64) + y2, 1e-5, "linearity")
+    assert np.all(run_gemv(qmm, w, np.zeros((1, K), np.float32)) == 0.0)
+
+
+def test_gemv_repeatable(qmm):
+    N, K = 4096, 4096
+    blocks = synth.weight_blocks(Q4_0, N, K, seed=3)
+    w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
+    x = synth.normal(4, (1, K), 1.0)
+    a, b = run_gemv(qmm, w, x), run_gemv(qmm, w, x)
+    assert np.array_equal(a, b)  # fixed reduction order: bitwise deterministic
+
+
+def test_gemv_error_paths(qmm):
+    from openmini_qmm import _native
+    blocks = synth.weight_blocks(Q4_0, 8, 64, seed=1)
+    w = qmm.QuantizedWeight(Q4_0, blocks, 8, 64)
+    dx = qmm.DeviceBuffer(1024)
+    dy = qmm.DeviceBuffer(1024)
+    L = _native.lib()
+    assert L.openmini_qmm_gemv(w.handle, dx.ptr, dy.ptr, 0, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemv(w.handle, ctypes.c_void_p(dx.ptr.value + 4), dy.ptr, 1, None) \
+        == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemv(None, dx.ptr, dy.ptr, 1, None) == _native.ERR_INVALID_PARAM
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_engine_matmul_and_linear(qmm, orc, qtype):
+    """GemmEngine-shaped host API (linear / linear_gemm, model.rs:1050-1064)."""
+    N, K, M = 200, 1024, 21
+    blocks = synth.weight_blocks(qtype, N, K, seed=31)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(32, (M, K), 1.0)
+    ref = orc.linear_f64(qtype, blocks, N, K, x)
+    eng = qmm.get_gemm_engine()
+    assert eng.is_available() and eng.name() == "hip_quant"
+    assert_parity(eng.matmul(x, w), ref, TOL, "matmul")
+    assert_parity(qmm.linear(x, w), ref, TOL, "linear")
+    assert_parity(qmm.linear_gemm(x[:1], w), ref[:1], TOL, "linear_gemm")
+    with pytest.raises(qmm.InvalidInput):
+        eng.matmul(x[:, :512], w)

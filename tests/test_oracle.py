@@ -1,0 +1,304 @@
+"""Pins the CPU oracle (oracle/qmm_oracle.c) before any GPU result is compared to it.
+
+Each check is chosen so a plausible mistake fails it: the reference's own known
+answers (tests/golden/reference_kats.json, transcribed with file:line), exhaustive
+or library comparisons for the float conversions (numpy float16), an asymmetric
+nibble KAT for the element order the reference source fixes, hand-computed
+quantizer blocks, and numpy float64 matmul for the contraction.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from openmini_qmm import synth
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+KATS = json.load(open(os.path.join(GOLDEN, "reference_kats.json")))
+Q4_0, Q8_0 = 2, 7
+
+
+# ---- float conversions ----------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([orc.f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(orc):
+    rng = np.random.default_rng(7)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25,
+                  1.5 * 2.0 ** -25, 2.0 ** -14, 0.1, 0.2, 100.0, np.inf, -np.inf], dtype=np.float32),
+        # exact halfway cases between fp16 neighbours
+        (np.arange(1, 2000, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([orc.f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_f32_to_bf16_rne(orc):
+    # hand-checked: ties to even on both sides, carry into the exponent
+    cases = {0x3F800000: 0x3F80, 0x3F808000: 0x3F80, 0x3F818000: 0x3F82, 0x3F808001: 0x3F81,
+             0x3F7FFFFF: 0x3F80, 0x7F7FFFFF: 0x7F80, 0x80000000: 0x8000, 0xBF808000: 0xBF80}
+    for f_bits, b in cases.items():
+        f = np.array([f_bits], dtype=np.uint32).view(np.float32)[0]
+        assert orc.f32_to_bf16(float(f)) == b
+        assert int(synth.to_bf16_bits(np.array([f]))[0]) == b
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(5000).astype(np.float32)
+    assert np.array_equal(orc.f32_to_bf16_array(v), synth.to_bf16_bits(v))
+
+
+# ---- reference known answers ------------------------------------------------------------
+
+@pytest.mark.parametrize("case", KATS["dequantize"], ids=lambda c: c["src"].split()[-1])
+def test_reference_dequantize_kats(orc, case):
+    data = bytes.fromhex(case["hex"])
+    out = orc.dequantize(case["type"], data, case["n"])
+    assert out.size == case["expect_len"]
+    if "expect_prefix" in case:
+        exp = np.array(case["expect_prefix"], dtype=np.float32)
+        assert np.all(np.abs(out[: exp.size] - exp) <= case["tol"])
+    if case.get("all_zero"):
+        assert np.all(out == 0.0)
+    if "all_value" in case:
+        assert np.all(out == np.float32(case["all_value"]))
+
+
+@pytest.mark.parametrize("case", KATS["safe_dequantize"], ids=lambda c: c["src"].split()[1])
+def test_reference_safe_dequantize_kats(orc, case):
+    data = bytes.fromhex(case["hex"])
+    st, out, expected = orc.safe_dequantize(case["type"], data, case["n"])
+    if case["ok"]:
+        assert st == 0 and out.size == case["expect_len"]
+        if "abs_below" in case:
+            assert np.all(np.isfinite(out)) and np.all(np.abs(out) < case["abs_below"])
+    else:
+        assert st == 1 and expected == case["expected"] and len(data) == case["actual"]
+
+
+def test_reference_truncated_inputs(orc):
+    spec = KATS["truncated"]
+    full = orc.create_test_q4_0_data(spec["n"])
+    assert full.size == 36
+    for ln in spec["lengths"]:
+        st, _, expected = orc.safe_dequantize(Q4_0, full[:ln], spec["n"])
+        if ln >= spec["ok_from"]:
+            assert st == 0
+        else:
+            assert st == 1 and expected == 36
+
+
+def test_reference_non_aligned_sizes(orc):
+    for n in KATS["non_aligned_sizes"]["sizes"]:
+        for qt, gen in ((Q4_0, orc.create_test_q4_0_data), (Q8_0, orc.create_test_q8_0_data)):
+            st, out, _ = orc.safe_dequantize(qt, gen(n), n)
+            assert st == 0 and out.size == n and np.all(np.isfinite(out))
+
+
+def test_unsupported_type(orc):
+    # tests/quant_simd_regression_test.rs:271-273: safe_dequantize(&[], Q2K, 32) is an error
+    st, _, _ = orc.safe_dequantize(10, b"", 32)
+    assert st == 2
+
+
+@pytest.mark.parametrize("case", KATS["geometry"], ids=lambda c: str(c["type"]))
+def test_reference_geometry(orc, case):
+    L = orc.lib()
+    assert L.orc_bytes_per_block(case["type"]) == case["bytes_per_block"]
+    assert L.orc_block_size(case["type"]) == case["block_size"]
+
+
+def test_data_size_closed_form(orc):
+    for qt, bpb in ((Q4_0, 18), (Q8_0, 34)):
+        for n in (0, 1, 31, 32, 33, 4096 * 4096, 4096 * 11008):
+            assert orc.data_size(qt, n) == (n + 31) // 32 * bpb
+    assert orc.data_size(Q4_0, 4096 * 11008) == 25_362_432
+    assert orc.data_size(Q8_0, 4096 * 11008) == 47_906_816
+
+
+@pytest.mark.parametrize("case", KATS["f16"], ids=lambda c: c["src"].split()[-1])
+def test_reference_f16_kats(orc, case):
+    for b, v in zip(case["bits"], case["values"]):
+        assert orc.f16_to_f32(b) == v
+
+
+def test_q4_0_nibble_order_asymmetric(orc):
+    # quant.rs:179-188: element 2j = (qs[j] >> 4) - 8, element 2j+1 = (qs[j] & 0xF) - 8.
+    blk = bytes([0x00, 0x3C, 0x1F, 0xA0]) + bytes(14)  # d = 1.0
+    out = orc.dequantize(Q4_0, blk, 32)
+    assert out[:4].tolist() == [1 - 8, 15 - 8, 10 - 8, 0 - 8]
+    assert np.all(out[4:] == -8.0)
+    # a scale of 0.5 (0x3800) multiplies once: (q - 8) * 0.5
+    blk = bytes([0x00, 0x38, 0x9E]) + bytes(15)
+    out = orc.dequantize(Q4_0, blk, 2)
+    assert out.tolist() == [0.5, 3.0]
+
+
+def test_q8_0_sign_and_scale(orc):
+    blk = bytes([0x00, 0xC0]) + bytes([0x80, 0x7F, 0xFF, 0x01]) + bytes(28)  # d = -2.0
+    out = orc.dequantize(Q8_0, blk, 4)
+    assert out.tolist() == [256.0, -254.0, 2.0, -2.0]
+
+
+def _numpy_dequant(qtype, data, n):
+    """Vectorised restatement (independent of the C loop structure)."""
+    bpb = 18 if qtype == Q4_0 else 34
+    nblk = len(data) // bpb
+    a = np.frombuffer(bytes(data[: nblk * bpb]), dtype=np.uint8).reshape(nblk, bpb)
+    d = a[:, :2].copy().view(np.float16).astype(np.float32)
+    if qtype == Q4_0:
+        q = np.empty((nblk, 32), dtype=np.int32)
+        q[:, 0::2] = (a[:, 2:] >> 4).astype(np.int32) - 8
+        q[:, 1::2] = (a[:, 2:] & 15).astype(np.int32) - 8
+    else:
+        q = a[:, 2:].view(np.int8).astype(np.int32)
+    out = np.zeros(n, dtype=np.float32)
+    v = (q.astype(np.float32) * d).ravel()
+    m = min(n, v.size)
+    out[:m] = v[:m]
+    return out
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_dequant_vs_vectorised_restatement(orc, qtype):
+    rng = np.random.default_rng(11)
+    gen = orc.create_test_q4_0_data if qtype == Q4_0 else orc.create_test_q8_0_data
+    for n in (1, 33, 1000, 4096):
+        data = gen(n)
+        assert np.array_equal(orc.dequantize(qtype, data, n).view(np.uint32),
+                              _numpy_dequant(qtype, data, n).view(np.uint32))
+    bpb = 18 if qtype == Q4_0 else 34
+    raw = rng.integers(0, 256, 64 * bpb, dtype=np.uint8)
+    raw[1::bpb] &= 0x7B  # keep scales finite
+    for n in (64 * 32, 64 * 32 - 5):
+        assert np.array_equal(orc.dequantize(qtype, raw, n).view(np.uint32),
+                              _numpy_dequant(qtype, raw, n).view(np.uint32))
+
+
+# ---- SoA repack (the reference's only layout conversion) ---------------------------------
+
+@pytest.mark.parametrize("case", KATS["soa"], ids=lambda c: str(c["type"]))
+def test_reference_soa_kats(orc, case):
+    data = bytes.fromhex(case["block_hex"]) * case["blocks"]
+    soa = orc.convert_to_soa(case["type"], data, case["n"])
+    assert soa.size == case["expect_len"]
+    if "expect_prefix_hex" in case:
+        p = bytes.fromhex(case["expect_prefix_hex"])
+        assert bytes(soa[: len(p)]) == p
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_soa_is_the_position_major_permutation(orc, qtype):
+    bpb = 18 if qtype == Q4_0 else 34
+    nblk = 7
+    raw = np.random.default_rng(5).integers(0, 256, nblk * bpb, dtype=np.uint8)
+    soa = orc.convert_to_soa(qtype, raw, nblk * 32)
+    blocks = raw.reshape(nblk, bpb)
+    assert np.array_equal(soa[: 2 * nblk].reshape(nblk, 2), blocks[:, :2])
+    assert np.array_equal(soa[2 * nblk:].reshape(bpb - 2, nblk), blocks[:, 2:].T)
+    short = orc.convert_to_soa(qtype, raw[: bpb + 3], 2 * 32)  # missing bytes read as 0
+    assert short.size == 2 * bpb and short[2] == raw[bpb] and short[3] == raw[bpb + 1]
+    assert orc.convert_to_soa(qtype, b"", 32).size == 0
+
+
+# ---- synthetic-weight quantizers ---------------------------------------------------------
+
+def test_q4_0_quantizer_hand_block(orc):
+    x = np.zeros(32, dtype=np.float32)
+    x[0], x[1], x[2], x[3] = -0.8, 0.7, 0.05, -0.05
+    blk = orc.quantize(Q4_0, x)
+    d = blk[:2].copy().view(np.float16)[0]
+    assert d == np.float16(0.1)                   # d = max / -8 with max = -0.8
+    # codes: -0.8*10+8.5=0.5->0, 0.7*10+8.5=15.5->15, 0.05*10+8.5=9.0->9, -0.5+8.5=8.0->8
+    assert blk[2] == (0 << 4) | 15 and blk[3] == (9 << 4) | 8
+    assert np.all(blk[4:] == 0x88)
+    assert np.array_equal(blk, synth.quantize_q4_0(x))
+
+
+def test_q8_0_quantizer_hand_block(orc):
+    x = np.zeros(32, dtype=np.float32)
+    x[0], x[1], x[2], x[3] = 127.0, 2.5, -2.5, -0.4999
+    blk = orc.quantize(Q8_0, x)
+    assert blk[0] == 0x00 and blk[1] == 0x3C      # d = 1.0
+    assert blk[2:6].view(np.int8).tolist() == [127, 3, -3, 0]  # round half away from zero
+    assert np.array_equal(blk, synth.quantize_q8_0(x))
+    assert np.all(orc.quantize(Q8_0, np.zeros(32, np.float32))[2:] == 0)
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_quantizer_round_trip_bounds(orc, qtype):
+    x = synth.normal(123, (64, 256), 0.02)
+    blocks = orc.quantize(qtype, x)
+    assert np.array_equal(blocks, synth.quantize(qtype, x))
+    w = orc.dequantize(qtype, blocks, x.size).reshape(-1, 32)
+    d = np.abs(blocks.reshape(-1, 18 if qtype == Q4_0 else 34)[:, :2].copy().view(np.float16)
+               .astype(np.float32))
+    err = np.abs(w - x.reshape(-1, 32))
+    # rounding to the nearest code (Q4_0: a value at -max clamps from code 16 to 15,
+    # a full step), plus the fp16 rounding of the scale (<= 2^-11 relative)
+    steps = 8.0 if qtype == Q4_0 else 127.0
+    half = 1.0 if qtype == Q4_0 else 0.5
+    assert np.all(err <= d * (half + steps * 2.0 ** -10))
+    if qtype == Q4_0:
+        assert np.mean(err <= d * (0.5 + steps * 2.0 ** -10)) > 0.99
+
+
+# ---- the contraction -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_linear_f64_matches_numpy_float64(orc, qtype):
+    N, K, B = 40, 256, 3
+    blocks = synth.weight_blocks(qtype, N, K, seed=9)
+    x = synth.normal(10, (B, K), 1.0)
+    w = orc.dequantize(qtype, blocks, N * K).reshape(N, K).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T
+    got = orc.linear_f64(qtype, blocks, N, K, x)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    xb = synth.to_bf16_bits(x)
+    got_b = orc.linear_bf16x_f64(qtype, blocks, N, K, xb)
+    ref_b = synth.bf16_bits_to_f32(xb).astype(np.float64) @ w.T
+    assert np.allclose(got_b, ref_b, rtol=1e-12, atol=1e-12)
+
+
+def test_linear_closed_form(orc):
+    # every code 0x99 -> q = 9 - 8 = 1, d = 0.5: w = 0.5 everywhere; x = 1 -> y = 0.5 K
+    K, N = 96, 3
+    blocks = (bytes([0x00, 0x38]) + bytes([0x99]) * 16) * (N * K // 32)
+    y = orc.linear_f64(Q4_0, np.frombuffer(blocks, np.uint8), N, K, np.ones((1, K), np.float32))
+    assert np.all(y == 0.5 * K)
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_cpu_baselines_agree_with_oracle(orc, qtype):
+    N, K = 64, 512
+    blocks = synth.weight_blocks(qtype, N, K, seed=21)
+    x = synth.normal(22, (2, K), 1.0)
+    ref = orc.linear_f64(qtype, blocks, N, K, x)
+    w = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
+    scratch = np.empty(N * K, dtype=np.float32)
+    for tc in (False, True):
+        y = orc.cpu_asrun_linear(w, x, scratch, tc)
+        assert np.max(np.abs(y - ref)) <= 1e-4 * np.max(np.abs(ref))
+    y = np.empty((2, N), dtype=np.float32)
+    orc.cpu_fused_linear(qtype, blocks, N, K, x, y, 0, N)
+    assert np.max(np.abs(y - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+def test_golden_regression(orc):
+    """Committed oracle outputs (tests/golden/make_golden.py) still reproduce."""
+    g = np.load(os.path.join(GOLDEN, "oracle_small.npz"))
+    for qtype, tag in ((Q4_0, "q4"), (Q8_0, "q8")):
+        blocks, x = g[f"{tag}_blocks"], g[f"{tag}_x"]
+        N, K = g[f"{tag}_shape"]
+        assert np.array_equal(orc.linear_f64(qtype, blocks, int(N), int(K), x), g[f"{tag}_y"])
+        assert np.array_equal(orc.dequantize(qtype, blocks, int(N * K)), g[f"{tag}_w"])
