@@ -10,8 +10,10 @@ Infinity Cache.  Inputs are resident in HBM before timing starts.
 
 `value` = algorithmic bytes per step (W bytes + x + y) x steps / wall time of the
 timed region (HIP events on the launch stream, device synchronised on both sides).
-`roofline.achieved` uses the average duration of a single GEMV launch, from an
-event pair around each launch over a second timed pass.  The Q8_0 prefill GEMM
+The timed launches are captured once in a HIP graph and replayed, so host launch
+cost is excluded; `roofline.achieved` divides the same bytes by the average launch
+duration over the timed region (region time / launches, which includes the
+graph's back-to-back dispatch gap).  The Q8_0 prefill GEMM
 (W[11008, 4096], M = 512, bf16 X) is measured the same way and reported under
 "gemm".  `cpu_baseline` times the reference's per-token CPU path (f32 GEMV over
 weights dequantized at load, one thread, restated in oracle/) on the host cores.
@@ -42,29 +44,19 @@ def log(msg: str) -> None:
 
 
 def time_steps(launch, steps: int, stream, hipr) -> float:
-    """Wall time (ms) of `steps` back-to-back launches between events on `stream`."""
+    """Wall time (ms) of `steps` back-to-back launches replayed from one HIP graph
+    (captured once, so host launch cost is not what is measured), between events
+    on `stream`, with the device synchronised on both sides."""
+    graph = hipr.Graph(stream, lambda s: [launch(i) for i in range(steps)])
+    graph.launch(stream)  # untimed replay
     hipr.hip().hipDeviceSynchronize()
     e0, e1 = hipr.Event(), hipr.Event()
     e0.record(stream)
-    for i in range(steps):
-        launch(i)
+    graph.launch(stream)
     e1.record(stream)
     e1.synchronize()
     hipr.hip().hipDeviceSynchronize()
     return e0.elapsed_ms(e1)
-
-
-def time_each_launch(launch, steps: int, stream, hipr) -> float:
-    """Average duration (ms) of one launch, from an event pair around each launch."""
-    hipr.hip().hipDeviceSynchronize()
-    evs = [(hipr.Event(), hipr.Event()) for _ in range(steps)]
-    for i, (a, b) in enumerate(evs):
-        a.record(stream)
-        launch(i)
-        b.record(stream)
-    evs[-1][1].synchronize()
-    hipr.hip().hipDeviceSynchronize()
-    return float(np.mean([a.elapsed_ms(b) for a, b in evs]))
 
 
 def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed=0x5EED0001):
@@ -93,7 +85,7 @@ def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed
     if not np.array_equal(dy.download(np.float32, (batch, N)), dy_check.download(np.float32, (batch, N))):
         raise RuntimeError("GEMV copies disagree")
     total_ms = time_steps(launch, steps, sh, hipr)
-    per_launch_ms = time_each_launch(launch, steps, sh, hipr)
+    per_launch_ms = total_ms / steps
     alg_bytes = wbytes + batch * K * 4 + batch * N * 4
     res = {
         "N": N, "K": K, "batch": batch, "weight_bytes": wbytes, "alg_bytes_per_step": alg_bytes,
@@ -126,7 +118,7 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
         launch(i)
     stream.synchronize()
     total_ms = time_steps(launch, steps, sh, hipr)
-    per_launch_ms = time_each_launch(launch, steps, sh, hipr)
+    per_launch_ms = total_ms / steps
     flops = 2.0 * M * N * K
     for w in ws:
         w.close()

@@ -127,7 +127,8 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
  * gemm_engine.rs:40), on the quantized W without materialising f32 weights. */
 
 /* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
- * Any batch >= 1 (HBM-bound up to 8; larger batches run in slices of 8 rows).
+ * Any batch >= 1; launches cover 4 activation rows each (weights are read once
+ * per launch), so batches above 4 re-read W once per 4 rows.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);

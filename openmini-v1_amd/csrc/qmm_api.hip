@@ -87,6 +87,15 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
     if (n_rows > INT32_MAX || k_cols / qmm::kQK > INT32_MAX / 64)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld] too large", (long long)n_rows,
                     (long long)k_cols);
+    // The decode kernels address codes with 32-bit buffer offsets: the tiled code
+    // array (padding included) must stay below 4 GiB (a Q4_0 matrix of ~7.5 G
+    // elements; the largest Llama-70B projection is 0.23 G).
+    const size_t tiled = (size_t)((n_rows + qmm::kTileRows - 1) / qmm::kTileRows) * qmm::kTileRows *
+                         (size_t)((k_cols / qmm::kQK + qmm::kTileBlocks - 1) / qmm::kTileBlocks) *
+                         qmm::kTileBlocks * qmm::code_bytes_per_block(type);
+    if (tiled >= ((size_t)1 << 32))
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld]: %zu code bytes exceed 4 GiB",
+                    (long long)n_rows, (long long)k_cols, tiled);
     const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
     if (gguf_bytes < need)
         return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA,
@@ -103,9 +112,11 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     w.n = n_rows;
     w.k = k_cols;
     w.nb = k_cols / qmm::kQK;
-    const size_t nblocks = (size_t)w.n * (size_t)w.nb;
-    const size_t code_bytes = round_up(nblocks * qmm::code_bytes_per_block(type), 256);
-    const size_t scale_bytes = round_up(nblocks * 2, 256);
+    w.n_tiles = (w.n + qmm::kTileRows - 1) / qmm::kTileRows;
+    w.groups = (w.nb + qmm::kTileBlocks - 1) / qmm::kTileBlocks;
+    const size_t entries = (size_t)w.entries();
+    const size_t code_bytes = round_up(entries * qmm::code_bytes_per_block(type), 256);
+    const size_t scale_bytes = round_up(entries * 2, 256);
     w.device_bytes = code_bytes + scale_bytes;
     hipError_t e = hipMalloc(&w.base, w.device_bytes);
     if (e != hipSuccess) {
@@ -117,6 +128,13 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     w.scales = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(w.base) + code_bytes);
     *out = h;
     return OPENMINI_QMM_OK;
+}
+
+// Zeroes the tile padding (rows past n, blocks past nb) before the repack fills
+// the rest; nothing to do when the shape tiles exactly.
+hipError_t clear_padding(const qmm::Weight& w, hipStream_t s) {
+    if (w.n % qmm::kTileRows == 0 && w.nb % qmm::kTileBlocks == 0) return hipSuccess;
+    return hipMemsetAsync(w.base, 0, w.device_bytes, s);
 }
 
 int check_weight(const openmini_qweight* h) {
@@ -212,9 +230,8 @@ int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes, in
         return rc;
     }
     e = hipMemcpy(staging, gguf_blocks, need, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = qmm::launch_repack(type, static_cast<const uint8_t*>(staging), n_rows * (k_cols / qmm::kQK),
-                               h->w.codes, h->w.scales, nullptr);
+    if (e == hipSuccess) e = clear_padding(h->w, nullptr);
+    if (e == hipSuccess) e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(staging), nullptr);
     if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
     (void)hipFree(staging);
     if (e != hipSuccess) {
@@ -238,9 +255,9 @@ int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_
     openmini_qweight* h = nullptr;
     rc = alloc_weight(type, n_rows, k_cols, dev, &h);
     if (rc != OPENMINI_QMM_OK) return rc;
-    hipError_t e = qmm::launch_repack(type, static_cast<const uint8_t*>(d_gguf_blocks),
-                                      n_rows * (k_cols / qmm::kQK), h->w.codes, h->w.scales,
-                                      as_stream(stream));
+    hipError_t e = clear_padding(h->w, as_stream(stream));
+    if (e == hipSuccess)
+        e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(d_gguf_blocks), as_stream(stream));
     if (e != hipSuccess) {
         openmini_qmm_free_weight(h);
         return hip_fail(e, "repack launch");
@@ -282,8 +299,8 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
     if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
     const qmm::Weight& w = weight->w;
-    for (int64_t b0 = 0; b0 < batch; b0 += 8) {
-        const int nb = (int)((batch - b0) < 8 ? (batch - b0) : 8);
+    for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
+        const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
         hipError_t e = qmm::launch_gemv(w, d_x + b0 * w.k, d_y + b0 * w.n, nb, as_stream(stream));
         if (e != hipSuccess) return hip_fail(e, "gemv launch");
     }
@@ -317,8 +334,8 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
         return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
     }
     e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
-    for (int64_t b0 = 0; e == hipSuccess && b0 < m; b0 += 8) {
-        const int nb = (int)((m - b0) < 8 ? (m - b0) : 8);
+    for (int64_t b0 = 0; e == hipSuccess && b0 < m; b0 += qmm::kMaxGemvBatch) {
+        const int nb = (int)((m - b0) < qmm::kMaxGemvBatch ? (m - b0) : qmm::kMaxGemvBatch);
         e = qmm::launch_gemv(w, static_cast<const float*>(dx) + b0 * w.k, static_cast<float*>(dy) + b0 * w.n,
                              nb, nullptr);
     }

@@ -10,9 +10,11 @@
 // Weights are never rounded (no bf16 q*d), activations are not requantized.
 //
 // Tiling: a 256-thread workgroup computes a 128 x 128 tile of y; its four waves
-// each own 64 x 64 (4 x 4 MFMA subtiles).  Per K step of 64 (two blocks) the
-// workgroup stages X[128][64] bf16 and the 128 code rows in LDS (rows padded to
-// dodge bank conflicts); each wave converts its B fragments from LDS codes.
+// each own 64 x 64 (4 x 4 MFMA subtiles).  A K step is one 4-block group (128
+// elements): the workgroup stages X[128][128] bf16 (rows padded against bank
+// conflicts) and the group's eight 16-row weight tiles -- contiguous 1 KB / 2 KB
+// runs of the tiled layout -- in LDS; each wave converts its B fragments from the
+// LDS codes.
 #include "qmm_internal.hpp"
 
 namespace qmm {
@@ -22,25 +24,22 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kKStep = 64;                     // elements per LDS stage (2 blocks)
-constexpr int kXRowBytes = kKStep * 2 + 16;    // 144: padded bf16 row
+constexpr int kBN = 128;                       // 8 weight tiles
+constexpr int kNT = kBN / kTileRows;
+constexpr int kKStep = kTileBlocks * kQK;      // 128 elements per LDS stage
+constexpr int kXRowBytes = kKStep * 2 + 16;    // 272: padded bf16 row
 constexpr int kThreads = 256;
-
-template <bool kQ4>
-struct CodeTile {
-    static constexpr int kRowBytes = kQ4 ? 36 : 72;  // 32 / 64 code bytes + pad
-};
 
 __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     // bf16 of exactly-representable values = high halves of their fp32 bits.
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// 8 Q4_0 nibbles (one code word) -> 8 bf16 (q-8)/16 in k order.
+// 8 Q4_0 nibbles (one code word, elements in order) -> 8 bf16 (q-8)/16.
 __device__ __forceinline__ bf16x8 cvt_q4(uint32_t w) {
+    w ^= 0x88888888u;  // nibbles now read as q - 8 in two's complement
     uint32_t h = w >> 4;
-    asm volatile("" : "+v"(h));
+    asm("" : "+v"(h));  // keep the shift: 1 shift + 4 SDWA converts, not 4 bit-field extracts
     const float a0 = __builtin_amdgcn_cvt_off_f32_i4(w & 0xFFu);
     const float a1 = __builtin_amdgcn_cvt_off_f32_i4((w >> 8) & 0xFFu);
     const float a2 = __builtin_amdgcn_cvt_off_f32_i4((w >> 16) & 0xFFu);
@@ -71,19 +70,19 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
                                                         const uint8_t* __restrict__ codes,
                                                         const uint16_t* __restrict__ scales,
                                                         float* __restrict__ y, int m_rows,
-                                                        int n_rows, int nb, int k) {
-    constexpr int kCB = kQ4 ? 16 : 32;            // code bytes per block
-    constexpr int kCRow = CodeTile<kQ4>::kRowBytes;
+                                                        int n_rows, int n_tiles, int groups, int k) {
+    constexpr int kCB = kQ4 ? 16 : 32;             // code bytes per entry
+    constexpr int kTileBytes = kTileEntries * kCB;  // 1 KB / 2 KB
     __shared__ __attribute__((aligned(16))) uint8_t xs[kBM * kXRowBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t cs[kBN * kCRow];
-    __shared__ float ds[kBN][2];
+    __shared__ __attribute__((aligned(16))) uint8_t cs[kNT * kTileBytes];
+    __shared__ float ds[kNT][kTileEntries];
 
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kBM;
-    const int n0 = blockIdx.x * kBN;
+    const int tile0 = blockIdx.x * kNT;
     const int li = lane & 15;   // row of A / column of B inside a 16 x 16 subtile
     const int lk = lane >> 4;   // which 8-element k group of the 32-element block
 
@@ -93,57 +92,59 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int b0 = 0; b0 < nb; b0 += 2) {
-        const int nblk = (nb - b0) >= 2 ? 2 : 1;
-        // ---- stage X[128][64] bf16: thread t loads 64 B = half a row -------------
-        {
-            const int r = t >> 1, h = t & 1;
+    for (int g = 0; g < groups; ++g) {
+        // ---- stage X[128][128] bf16: 8 x 16 B per thread -------------------------------
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = t + i * kThreads;        // 16-byte piece: row q / 16, piece q % 16
+            const int r = q >> 4, p = q & 15;
             const int gm = min(m0 + r, m_rows - 1);
-            uint4* dst = reinterpret_cast<uint4*>(xs + r * kXRowBytes + h * 64);
-            if (h < nblk) {
-                const uint4* src =
-                    reinterpret_cast<const uint4*>(x + (size_t)gm * k + (size_t)(b0 + h) * kQK);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) dst[i] = src[i];
-            }
+            const int kk = g * kKStep + p * 8;     // first element of the piece
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (kk < k) v = *reinterpret_cast<const uint4*>(x + (size_t)gm * k + kk);
+            *reinterpret_cast<uint4*>(xs + r * kXRowBytes + p * 16) = v;
         }
-        // ---- stage codes of 128 rows x nblk blocks and their scales -----------------
-        {
-            const int r = t >> 1, h = t & 1;
-            const int gn = min(n0 + r, n_rows - 1);
-            if (h < nblk) {
-                const size_t bi = (size_t)gn * nb + b0 + h;
-                const uint32_t* src = reinterpret_cast<const uint32_t*>(codes + bi * kCB);
-                uint32_t* dst = reinterpret_cast<uint32_t*>(cs + r * kCRow + h * kCB);
+        // ---- stage the group's 8 weight tiles and their scales -------------------------
 #pragma unroll
-                for (int i = 0; i < kCB / 4; ++i) dst[i] = src[i];
-                float d = f16_bits_to_f32(scales[bi]);
-                if constexpr (kQ4) d *= 16.0f;
-                ds[r][h] = d;
-            }
+        for (int i = 0; i < kNT * kTileBytes / 16 / kThreads; ++i) {
+            const int q = t + i * kThreads;        // 16-byte piece of the 8 tiles
+            const int tl = q / (kTileBytes / 16), p = q % (kTileBytes / 16);
+            const int64_t tile = min(tile0 + tl, n_tiles - 1);
+            const uint4* src = reinterpret_cast<const uint4*>(
+                codes + ((tile * groups + g) * kTileEntries) * (int64_t)kCB);
+            reinterpret_cast<uint4*>(cs)[q] = src[p];
+        }
+        for (int q = t; q < kNT * kTileEntries; q += kThreads) {
+            const int tl = q / kTileEntries, e = q % kTileEntries;
+            const int64_t tile = min(tile0 + tl, n_tiles - 1);
+            float d = f16_bits_to_f32(scales[(tile * groups + g) * kTileEntries + e]);
+            if constexpr (kQ4) d *= 16.0f;
+            ds[tl][e] = d;
         }
         __syncthreads();
 
-        for (int h = 0; h < nblk; ++h) {
+#pragma unroll
+        for (int bt = 0; bt < kTileBlocks; ++bt) {  // block slot within the group
             bf16x8 a[4], bfr[4];
             float dsc[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = wm * 64 + i * 16 + li;
-                a[i] = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const uint4*>(xs + r * kXRowBytes + h * 64 + lk * 16));
+                a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                      xs + r * kXRowBytes + (bt * kQK + lk * 8) * 2));
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int c = wn * 64 + j * 16 + li;
-                const uint8_t* cp = cs + c * kCRow + h * kCB;
+                const int tl = wn * 4 + j;                 // the 16 columns are one weight tile
+                const int e = bt * kTileRows + li;         // entry (block slot bt, row li)
+                const uint8_t* cp = cs + tl * kTileBytes + e * kCB;
                 if constexpr (kQ4) {
                     bfr[j] = cvt_q4(*reinterpret_cast<const uint32_t*>(cp + lk * 4));
                 } else {
                     const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cp + lk * 8);
                     bfr[j] = cvt_q8(c32[0], c32[1]);
                 }
-                dsc[j] = ds[c][h];
+                dsc[j] = ds[tl][e];
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int gn = n0 + wn * 64 + j * 16 + li;
+            const int gn = (tile0 + wn * 4 + j) * kTileRows + li;
             if (gn >= n_rows) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -178,13 +179,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m,
                             hipStream_t s) {
     if (m <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((w.n + kBN - 1) / kBN), (unsigned)((m + kBM - 1) / kBM));
+    const dim3 grid((unsigned)((w.n_tiles + kNT - 1) / kNT), (unsigned)((m + kBM - 1) / kBM));
     if (w.type == OPENMINI_QMM_Q4_0)
         hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, s, x, w.codes, w.scales, y,
-                           (int)m, (int)w.n, (int)w.nb, (int)w.k);
+                           (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     else
         hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, s, x, w.codes, w.scales,
-                           y, (int)m, (int)w.n, (int)w.nb, (int)w.k);
+                           y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     return hipGetLastError();
 }
 

@@ -18,14 +18,15 @@ __device__ __forceinline__ uint32_t q4_code(const uint8_t* qs, int e) {
     return (e & 1) ? (b & 0x0Fu) : (b >> 4);
 }
 
-// One workgroup repacks kTile consecutive GGUF blocks.  Full tiles of a 16-byte
-// aligned source are staged through LDS with 16-byte loads (a tile is 4608 B for
-// Q4_0 and 8704 B for Q8_0, both multiples of 16); the last partial tile and
-// unaligned sources fall back to byte loads.
+// One workgroup repacks kTile consecutive GGUF blocks (row-major order).  Full
+// tiles of a 16-byte aligned source are staged through LDS with 16-byte loads (a
+// tile is 4608 B for Q4_0 and 8704 B for Q8_0, both multiples of 16); the last
+// partial tile and unaligned sources fall back to byte loads.  Each block's codes
+// (16 / 32 B) and scale then go to its entry of the tiled layout.
 template <int kBPB>
 __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict__ gguf,
-                                                       int64_t nblocks, int aligned16,
-                                                       uint8_t* __restrict__ codes,
+                                                       int64_t nblocks, int64_t nb, int64_t groups,
+                                                       int aligned16, uint8_t* __restrict__ codes,
                                                        uint16_t* __restrict__ scales) {
     __shared__ uint4 tile[kTile * kBPB / 16];
     uint8_t* t8 = reinterpret_cast<uint8_t*>(tile);
@@ -43,8 +44,9 @@ __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict
     const int t = threadIdx.x;
     if (t >= nblk) return;
     const uint8_t* b = t8 + t * kBPB;
-    const int64_t blk = blk0 + t;
-    scales[blk] = (uint16_t)(b[0] | (b[1] << 8));
+    const int64_t g = blk0 + t;
+    const int64_t e = tile_entry(g / nb, g % nb, groups);
+    scales[e] = (uint16_t)(b[0] | (b[1] << 8));
     const uint8_t* qs = b + 2;
     if constexpr (kBPB == 18) {
         uint32_t w[4];
@@ -53,60 +55,56 @@ __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict
             uint32_t v = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t lo = q4_code(qs, 8 * j + i) ^ 8u;
-                uint32_t hi = q4_code(qs, 8 * j + 4 + i) ^ 8u;
+                uint32_t lo = q4_code(qs, 8 * j + i);
+                uint32_t hi = q4_code(qs, 8 * j + 4 + i);
                 v |= (lo | (hi << 4)) << (8 * i);
             }
             w[j] = v;
         }
-        reinterpret_cast<uint4*>(codes)[blk] = make_uint4(w[0], w[1], w[2], w[3]);
+        reinterpret_cast<uint4*>(codes)[e] = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
         uint32_t w[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) |
                    ((uint32_t)qs[4 * j + 2] << 16) | ((uint32_t)qs[4 * j + 3] << 24);
-        uint4* c4 = reinterpret_cast<uint4*>(codes) + 2 * blk;
+        uint4* c4 = reinterpret_cast<uint4*>(codes) + 2 * e;
         c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
         c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
     }
 }
 
-// Repacked weight -> f32.  One thread per 8 consecutive elements of a row
+// Tiled weight -> f32 [n][k].  One thread per 8 consecutive elements of a row
 // (one Q4_0 code word / two Q8_0 code words); stores are 2 x float4, contiguous
 // across the wave.
-__global__ __launch_bounds__(256) void dequant_weight_q4(const uint32_t* __restrict__ codes,
-                                                         const uint16_t* __restrict__ scales,
-                                                         int64_t ngroups, float* __restrict__ out) {
+template <bool kQ4>
+__global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __restrict__ codes,
+                                                             const uint16_t* __restrict__ scales,
+                                                             int64_t nwords, int64_t nb,
+                                                             int64_t groups, float* __restrict__ out) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= ngroups) return;
-    const uint32_t w = codes[g];              // word g%4 of block g/4
-    const float d = f16_bits_to_f32(scales[g >> 2]);
-    const uint32_t hi = w >> 4;
+    if (g >= nwords) return;
+    const int64_t row = g / (nb * 4);
+    const int64_t rem = g - row * nb * 4;
+    const int64_t e = tile_entry(row, rem >> 2, groups);
+    const int j = (int)(rem & 3);
+    const float d = f16_bits_to_f32(scales[e]);
     float v[8];
+    if constexpr (kQ4) {
+        const uint32_t w = reinterpret_cast<const uint32_t*>(codes + e * 16)[j];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // (q - 8) exactly, then one fp32 multiply, as quant.rs:190.
-        v[i] = (__builtin_amdgcn_cvt_off_f32_i4((w >> (8 * i)) & 0xFFu) * 16.0f) * d;
-        v[4 + i] = (__builtin_amdgcn_cvt_off_f32_i4((hi >> (8 * i)) & 0xFFu) * 16.0f) * d;
-    }
-    float4* o = reinterpret_cast<float4*>(out) + 2 * g;
-    o[0] = make_float4(v[0], v[1], v[2], v[3]);
-    o[1] = make_float4(v[4], v[5], v[6], v[7]);
-}
-
-__global__ __launch_bounds__(256) void dequant_weight_q8(const uint2* __restrict__ codes,
-                                                         const uint16_t* __restrict__ scales,
-                                                         int64_t ngroups, float* __restrict__ out) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= ngroups) return;
-    const uint2 w = codes[g];                 // 8 bytes = group g%4 of block g/4
-    const float d = f16_bits_to_f32(scales[g >> 2]);
-    float v[8];
+        for (int i = 0; i < 4; ++i) {
+            // (q - 8) exactly, then one fp32 multiply, as quant.rs:190.
+            v[i] = (float)((int)((w >> (8 * i)) & 0xFu) - 8) * d;
+            v[4 + i] = (float)((int)((w >> (8 * i + 4)) & 0xFu) - 8) * d;
+        }
+    } else {
+        const uint2 w = reinterpret_cast<const uint2*>(codes + e * 32)[j];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = (float)(int8_t)(w.x >> (8 * i)) * d;
-        v[4 + i] = (float)(int8_t)(w.y >> (8 * i)) * d;
+        for (int i = 0; i < 4; ++i) {
+            v[i] = (float)(int8_t)(w.x >> (8 * i)) * d;
+            v[4 + i] = (float)(int8_t)(w.y >> (8 * i)) * d;
+        }
     }
     float4* o = reinterpret_cast<float4*>(out) + 2 * g;
     o[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -154,30 +152,30 @@ inline unsigned grid_for(int64_t items, int per_block) {
 
 }  // namespace
 
-hipError_t launch_repack(int type, const uint8_t* gguf, int64_t nblocks, uint8_t* codes,
-                         uint16_t* scales, hipStream_t s) {
+hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
+    const int64_t nblocks = w.n * w.nb;
     if (nblocks <= 0) return hipSuccess;
     const int aligned = ((uintptr_t)gguf % 16) == 0;
     const dim3 grid(grid_for(nblocks, kTile));
-    if (type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kTile), 0, s, gguf, nblocks, aligned,
-                           codes, scales);
+    if (w.type == OPENMINI_QMM_Q4_0)
+        hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
+                           w.groups, aligned, w.codes, w.scales);
     else
-        hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kTile), 0, s, gguf, nblocks, aligned,
-                           codes, scales);
+        hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
+                           w.groups, aligned, w.codes, w.scales);
     return hipGetLastError();
 }
 
 hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s) {
-    const int64_t ngroups = w.n * w.nb * 4;
-    if (ngroups == 0) return hipSuccess;
-    const dim3 grid(grid_for(ngroups, 256));
+    const int64_t nwords = w.n * w.nb * 4;
+    if (nwords == 0) return hipSuccess;
+    const dim3 grid(grid_for(nwords, 256));
     if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(dequant_weight_q4, grid, dim3(256), 0, s,
-                           reinterpret_cast<const uint32_t*>(w.codes), w.scales, ngroups, out);
+        hipLaunchKernelGGL(dequant_weight_kernel<true>, grid, dim3(256), 0, s, w.codes, w.scales,
+                           nwords, w.nb, w.groups, out);
     else
-        hipLaunchKernelGGL(dequant_weight_q8, grid, dim3(256), 0, s,
-                           reinterpret_cast<const uint2*>(w.codes), w.scales, ngroups, out);
+        hipLaunchKernelGGL(dequant_weight_kernel<false>, grid, dim3(256), 0, s, w.codes, w.scales,
+                           nwords, w.nb, w.groups, out);
     return hipGetLastError();
 }
 

@@ -53,6 +53,9 @@ def test_host_only_validation():
     assert L.openmini_qmm_upload(2, p, 20, 1, 64, ctypes.byref(h)) == _native.ERR_INSUFFICIENT_DATA
     assert b"expected 36" in L.openmini_qmm_last_error() and b"actual 20" in L.openmini_qmm_last_error()
     assert L.openmini_qmm_upload(3, p, 64, 1, 32, ctypes.byref(h)) == _native.ERR_UNSUPPORTED
+    # tiled codes must stay below 4 GiB (32-bit buffer offsets in the kernels)
+    assert L.openmini_qmm_upload(7, p, 64, 1 << 19, 8192, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
+    assert b"exceed 4 GiB" in L.openmini_qmm_last_error()
     # safe_dequantize semantics: n == 0 is Ok, short input reports expected bytes
     exp = ctypes.c_size_t(123)
     assert L.openmini_qmm_dequantize(2, None, 0, 0, None, ctypes.byref(exp)) == 0 and exp.value == 0
