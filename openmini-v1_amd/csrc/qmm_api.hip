@@ -87,15 +87,15 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
     if (n_rows > INT32_MAX || k_cols / qmm::kQK > INT32_MAX / 64)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld] too large", (long long)n_rows,
                     (long long)k_cols);
-    // The decode kernels address codes with 32-bit buffer offsets: the tiled code
-    // array (padding included) must stay below 4 GiB (a Q4_0 matrix of ~7.5 G
-    // elements; the largest Llama-70B projection is 0.23 G).
-    const size_t tiled = (size_t)((n_rows + qmm::kTileRows - 1) / qmm::kTileRows) * qmm::kTileRows *
-                         (size_t)((k_cols / qmm::kQK + qmm::kTileBlocks - 1) / qmm::kTileBlocks) *
-                         qmm::kTileBlocks * qmm::code_bytes_per_block(type);
-    if (tiled >= ((size_t)1 << 32))
-        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld]: %zu code bytes exceed 4 GiB",
-                    (long long)n_rows, (long long)k_cols, tiled);
+    // The decode kernels address the weight with 32-bit buffer offsets: the chunks
+    // (padding included) must stay below 4 GiB (a Q4_0 matrix of ~7.5 G elements; the
+    // largest Llama-70B projection is 0.23 G).
+    const size_t chunked = (size_t)((n_rows + qmm::kTileRows - 1) / qmm::kTileRows) *
+                           (size_t)((k_cols / qmm::kQK + qmm::kTileBlocks - 1) / qmm::kTileBlocks) *
+                           (size_t)qmm::chunk_bytes(type);
+    if (chunked >= ((size_t)1 << 32))
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld]: %zu weight bytes exceed 4 GiB",
+                    (long long)n_rows, (long long)k_cols, chunked);
     const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
     if (gguf_bytes < need)
         return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA,
@@ -114,18 +114,16 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     w.nb = k_cols / qmm::kQK;
     w.n_tiles = (w.n + qmm::kTileRows - 1) / qmm::kTileRows;
     w.groups = (w.nb + qmm::kTileBlocks - 1) / qmm::kTileBlocks;
-    const size_t entries = (size_t)w.entries();
-    const size_t code_bytes = round_up(entries * qmm::code_bytes_per_block(type), 256);
-    const size_t scale_bytes = round_up(entries * 2, 256);
-    w.device_bytes = code_bytes + scale_bytes;
-    hipError_t e = hipMalloc(&w.base, w.device_bytes);
+    w.chunk_bytes = (size_t)qmm::chunk_bytes(type);
+    w.device_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256);
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, w.device_bytes);
     if (e != hipSuccess) {
         delete h;
         return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) for weight failed: %s", w.device_bytes,
                     hipGetErrorString(e));
     }
-    w.codes = static_cast<uint8_t*>(w.base);
-    w.scales = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(w.base) + code_bytes);
+    w.chunks = static_cast<uint8_t*>(base);
     *out = h;
     return OPENMINI_QMM_OK;
 }
@@ -134,7 +132,7 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
 // the rest; nothing to do when the shape tiles exactly.
 hipError_t clear_padding(const qmm::Weight& w, hipStream_t s) {
     if (w.n % qmm::kTileRows == 0 && w.nb % qmm::kTileBlocks == 0) return hipSuccess;
-    return hipMemsetAsync(w.base, 0, w.device_bytes, s);
+    return hipMemsetAsync(w.chunks, 0, w.device_bytes, s);
 }
 
 int check_weight(const openmini_qweight* h) {
@@ -268,11 +266,11 @@ int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_
 
 void openmini_qmm_free_weight(openmini_qweight_t* weight) {
     if (!weight) return;
-    if (weight->w.base) {
+    if (weight->w.chunks) {
         int cur = 0;
         const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != weight->w.device;
         if (switch_dev) (void)hipSetDevice(weight->w.device);
-        (void)hipFree(weight->w.base);
+        (void)hipFree(weight->w.chunks);
         if (switch_dev) (void)hipSetDevice(cur);
     }
     delete weight;

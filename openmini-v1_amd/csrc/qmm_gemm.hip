@@ -35,9 +35,9 @@ __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// 8 Q4_0 nibbles (one code word, elements in order) -> 8 bf16 (q-8)/16.
+// 8 Q4_0 nibbles (one code word of two's-complement q - 8, elements in order) ->
+// 8 bf16 (q-8)/16.
 __device__ __forceinline__ bf16x8 cvt_q4(uint32_t w) {
-    w ^= 0x88888888u;  // nibbles now read as q - 8 in two's complement
     uint32_t h = w >> 4;
     asm("" : "+v"(h));  // keep the shift: 1 shift + 4 SDWA converts, not 4 bit-field extracts
     const float a0 = __builtin_amdgcn_cvt_off_f32_i4(w & 0xFFu);
@@ -67,12 +67,12 @@ __device__ __forceinline__ bf16x8 cvt_q8(uint32_t w0, uint32_t w1) {
 
 template <bool kQ4>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restrict__ x,
-                                                        const uint8_t* __restrict__ codes,
-                                                        const uint16_t* __restrict__ scales,
+                                                        const uint8_t* __restrict__ chunks,
                                                         float* __restrict__ y, int m_rows,
                                                         int n_rows, int n_tiles, int groups, int k) {
-    constexpr int kCB = kQ4 ? 16 : 32;             // code bytes per entry
-    constexpr int kTileBytes = kTileEntries * kCB;  // 1 KB / 2 KB
+    constexpr int kCB = kQ4 ? 16 : 32;             // code bytes per slot
+    constexpr int kTileBytes = kTileEntries * kCB;  // codes of a chunk: 1 KB / 2 KB
+    constexpr int kChunk = chunk_bytes_for(kQ4);
     __shared__ __attribute__((aligned(16))) uint8_t xs[kBM * kXRowBytes];
     __shared__ __attribute__((aligned(16))) uint8_t cs[kNT * kTileBytes];
     __shared__ float ds[kNT][kTileEntries];
@@ -110,14 +110,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restri
             const int q = t + i * kThreads;        // 16-byte piece of the 8 tiles
             const int tl = q / (kTileBytes / 16), p = q % (kTileBytes / 16);
             const int64_t tile = min(tile0 + tl, n_tiles - 1);
-            const uint4* src = reinterpret_cast<const uint4*>(
-                codes + ((tile * groups + g) * kTileEntries) * (int64_t)kCB);
+            const uint4* src = reinterpret_cast<const uint4*>(chunks + (tile * groups + g) * kChunk);
             reinterpret_cast<uint4*>(cs)[q] = src[p];
         }
         for (int q = t; q < kNT * kTileEntries; q += kThreads) {
             const int tl = q / kTileEntries, e = q % kTileEntries;
             const int64_t tile = min(tile0 + tl, n_tiles - 1);
-            float d = f16_bits_to_f32(scales[(tile * groups + g) * kTileEntries + e]);
+            const uint16_t* sc = reinterpret_cast<const uint16_t*>(chunks + (tile * groups + g) * kChunk + kTileBytes);
+            float d = f16_bits_to_f32(sc[e]);
             if constexpr (kQ4) d *= 16.0f;
             ds[tl][e] = d;
         }
@@ -181,11 +181,11 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
     if (m <= 0) return hipSuccess;
     const dim3 grid((unsigned)((w.n_tiles + kNT - 1) / kNT), (unsigned)((m + kBM - 1) / kBM));
     if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, s, x, w.codes, w.scales, y,
-                           (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+        hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, s, x, w.chunks, y, (int)m,
+                           (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     else
-        hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, s, x, w.codes, w.scales,
-                           y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+        hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, s, x, w.chunks, y, (int)m,
+                           (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     return hipGetLastError();
 }
 

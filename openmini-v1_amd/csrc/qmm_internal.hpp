@@ -4,28 +4,28 @@
 // -------------------------------------------------------------------------------
 // A GGUF Q4_0 / Q8_0 tensor W[N, K] arrives as N*nb blocks (nb = K/32), row-major,
 // each block = fp16 scale d followed by the codes (16 B of nibbles / 32 int8).
-// The upload splits codes from scales and regroups both into tiles of 16 rows x
-// 4 consecutive blocks (a "group" of 128 elements):
+// The upload regroups the blocks into tiles of 16 rows x 4 consecutive blocks (a
+// "group" of 128 elements).  One (row tile, group) pair is a chunk:
 //
-//   entry(row, blk) = ((row/16 * G + blk/4) * 64) + (blk%4) * 16 + row%16,  G = ceil(nb/4)
-//   codes : entry * 16 B (Q4_0) or * 32 B (Q8_0)      -> a tile is 1 KB / 2 KB, contiguous
-//   scales: entry * 2 B (fp16 bits)                   -> a tile is 128 B
+//   chunk c = (row/16) * G + blk/4,  G = ceil(nb/4),  slot e = (blk%4) * 16 + row%16
+//   chunk bytes: [64 x codes: e * 16 B (Q4_0) / e * 32 B (Q8_0)][64 x fp16 scale: e * 2 B]
+//   chunk size : 1152 B (Q4_0) / 2176 B (Q8_0), both multiples of 128 B
 //
-// Tiles follow each other along K, so the weight slice a wavefront sweeps is one
-// contiguous run of memory, and lane l of a wavefront reading a tile gets entry
-// l = (block slot t = l/16, row n = l%16): exactly the B-operand lane of a 16-wide
-// MFMA.  Rows are padded to a multiple of 16 and blocks to a multiple of 4 with
-// zero codes and zero scales; HBM bytes equal the GGUF bytes when N % 16 == 0 and
-// nb % 4 == 0 (all the Llama shapes).
+// Chunks follow each other along K, so the weight slice a wavefront sweeps -- codes
+// and scales -- is one contiguous run of memory, and lane l of a wavefront reading a
+// chunk gets slot l = (block slot t = l/16, row n = l%16): exactly the B-operand lane
+// of a 16-wide MFMA.  Rows are padded to a multiple of 16 and blocks to a multiple
+// of 4 with zero codes and zero scales; HBM bytes equal the GGUF bytes when
+// N % 16 == 0 and nb % 4 == 0 (all the Llama shapes).
 //
-// Inside an entry, Q8_0 codes keep GGUF order (int8).  Q4_0 codes (unsigned
-// 0..15, value q - 8) are permuted so a 32-bit word holds 8 consecutive elements:
+// Inside a slot, Q8_0 codes keep GGUF order (int8).  Q4_0 codes are stored as the
+// 4-bit two's-complement value s = q - 8 (the nibble q ^ 8) and permuted so a
+// 32-bit word holds 8 consecutive elements:
 //   word j (0..3), byte i (0..3): low nibble  = element 8j + i
 //                                 high nibble = element 8j + 4 + i
-// so w & 0x0F0F0F0F and (w >> 4) & 0x0F0F0F0F are elements 8j..8j+3 and
-// 8j+4..8j+7 as bytes, in order: ready-made int8 MFMA operands (3 VALU ops per
-// 8 weights).  XOR-ing a word with 0x88888888 makes each nibble's two's-complement
-// reading q - 8, which v_cvt_off_f32_i4 turns into (q - 8) / 16 in one op.
+// so (w << 4) & 0xF0F0F0F0 and w & 0xF0F0F0F0 are 16 * (q - 8) of elements
+// 8j..8j+3 and 8j+4..8j+7 as int8 bytes, in order (ready-made int8 MFMA operands),
+// and v_cvt_off_f32_i4 turns a nibble into (q - 8) / 16 in one op.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -52,12 +52,19 @@ inline int code_bytes_per_block(int type) {
 }
 
 constexpr int kTileRows = 16;   // rows per tile
-constexpr int kTileBlocks = 4;  // blocks per tile (one 128-element group)
-constexpr int kTileEntries = kTileRows * kTileBlocks;
+constexpr int kTileBlocks = 4;  // blocks per group
+constexpr int kTileEntries = kTileRows * kTileBlocks;  // slots per chunk
 
-// Index of (row, blk) in the tiled layout (entries, not bytes).
-__host__ __device__ __forceinline__ int64_t tile_entry(int64_t row, int64_t blk, int64_t groups) {
-    return (((row >> 4) * groups + (blk >> 2)) << 6) + ((blk & 3) << 4) + (row & 15);
+// Bytes of one chunk: 64 slots of codes, then their 64 fp16 scales.
+__host__ __device__ constexpr int chunk_bytes_for(bool q4) { return kTileEntries * (q4 ? 16 : 32) + 2 * kTileEntries; }
+inline int chunk_bytes(int type) { return chunk_bytes_for(type == OPENMINI_QMM_Q4_0); }
+
+// Chunk index and slot of (row, blk).
+__host__ __device__ __forceinline__ int64_t chunk_of(int64_t row, int64_t blk, int64_t groups) {
+    return (row >> 4) * groups + (blk >> 2);
+}
+__host__ __device__ __forceinline__ int slot_of(int64_t row, int64_t blk) {
+    return (int)(((blk & 3) << 4) + (row & 15));
 }
 
 struct Weight {
@@ -68,17 +75,16 @@ struct Weight {
     int64_t nb = 0;       // blocks per row
     int64_t n_tiles = 0;  // ceil(n / 16)
     int64_t groups = 0;   // ceil(nb / 4)
-    void* base = nullptr;        // single allocation: codes, then scales
-    uint8_t* codes = nullptr;    // tiled, code_bytes per entry
-    uint16_t* scales = nullptr;  // tiled, one fp16 per entry
+    uint8_t* chunks = nullptr;  // n_tiles * groups chunks, tile-major
+    size_t chunk_bytes = 0;
     size_t device_bytes = 0;
-    int64_t entries() const { return n_tiles * groups * kTileEntries; }
+    int64_t n_chunks() const { return n_tiles * groups; }
 };
 
 // ---- kernel launchers (qmm_repack.hip, qmm_gemv.hip, qmm_gemm.hip) ----------------
 
-// GGUF blocks (device, row-major [n][nb]) -> tiled codes + scales of `w` (whose
-// padding the caller has zeroed).
+// GGUF blocks (device, row-major [n][nb]) -> the chunks of `w` (whose padding the
+// caller has zeroed).
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s);
 
 // Repacked weight -> f32 [n][k].

@@ -22,12 +22,14 @@ __device__ __forceinline__ uint32_t q4_code(const uint8_t* qs, int e) {
 // tiles of a 16-byte aligned source are staged through LDS with 16-byte loads (a
 // tile is 4608 B for Q4_0 and 8704 B for Q8_0, both multiples of 16); the last
 // partial tile and unaligned sources fall back to byte loads.  Each block's codes
-// (16 / 32 B) and scale then go to its entry of the tiled layout.
+// (16 / 32 B) and scale then go to its slot of its chunk.
 template <int kBPB>
 __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict__ gguf,
                                                        int64_t nblocks, int64_t nb, int64_t groups,
-                                                       int aligned16, uint8_t* __restrict__ codes,
-                                                       uint16_t* __restrict__ scales) {
+                                                       int aligned16, uint8_t* __restrict__ chunks) {
+    constexpr bool kQ4 = kBPB == 18;
+    constexpr int kCB = kQ4 ? 16 : 32;
+    constexpr int kChunk = chunk_bytes_for(kQ4);
     __shared__ uint4 tile[kTile * kBPB / 16];
     uint8_t* t8 = reinterpret_cast<uint8_t*>(tile);
     const int64_t blk0 = (int64_t)blockIdx.x * kTile;
@@ -45,10 +47,12 @@ __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict
     if (t >= nblk) return;
     const uint8_t* b = t8 + t * kBPB;
     const int64_t g = blk0 + t;
-    const int64_t e = tile_entry(g / nb, g % nb, groups);
-    scales[e] = (uint16_t)(b[0] | (b[1] << 8));
+    const int64_t row = g / nb, blk = g % nb;
+    uint8_t* chunk = chunks + chunk_of(row, blk, groups) * kChunk;
+    const int e = slot_of(row, blk);
+    reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = (uint16_t)(b[0] | (b[1] << 8));
     const uint8_t* qs = b + 2;
-    if constexpr (kBPB == 18) {
+    if constexpr (kQ4) {
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -59,47 +63,50 @@ __global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict
                 uint32_t hi = q4_code(qs, 8 * j + 4 + i);
                 v |= (lo | (hi << 4)) << (8 * i);
             }
-            w[j] = v;
+            w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
         }
-        reinterpret_cast<uint4*>(codes)[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        reinterpret_cast<uint4*>(chunk)[e] = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
         uint32_t w[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) |
                    ((uint32_t)qs[4 * j + 2] << 16) | ((uint32_t)qs[4 * j + 3] << 24);
-        uint4* c4 = reinterpret_cast<uint4*>(codes) + 2 * e;
+        uint4* c4 = reinterpret_cast<uint4*>(chunk) + 2 * e;
         c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
         c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
     }
 }
 
-// Tiled weight -> f32 [n][k].  One thread per 8 consecutive elements of a row
+// Chunked weight -> f32 [n][k].  One thread per 8 consecutive elements of a row
 // (one Q4_0 code word / two Q8_0 code words); stores are 2 x float4, contiguous
 // across the wave.
 template <bool kQ4>
-__global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __restrict__ codes,
-                                                             const uint16_t* __restrict__ scales,
+__global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __restrict__ chunks,
                                                              int64_t nwords, int64_t nb,
                                                              int64_t groups, float* __restrict__ out) {
+    constexpr int kCB = kQ4 ? 16 : 32;
+    constexpr int kChunk = chunk_bytes_for(kQ4);
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nwords) return;
     const int64_t row = g / (nb * 4);
     const int64_t rem = g - row * nb * 4;
-    const int64_t e = tile_entry(row, rem >> 2, groups);
+    const int64_t blk = rem >> 2;
+    const uint8_t* chunk = chunks + chunk_of(row, blk, groups) * kChunk;
+    const int e = slot_of(row, blk);
     const int j = (int)(rem & 3);
-    const float d = f16_bits_to_f32(scales[e]);
+    const float d = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(chunk + kTileEntries * kCB)[e]);
     float v[8];
     if constexpr (kQ4) {
-        const uint32_t w = reinterpret_cast<const uint32_t*>(codes + e * 16)[j];
+        const uint32_t w = reinterpret_cast<const uint32_t*>(chunk + e * 16)[j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // (q - 8) exactly, then one fp32 multiply, as quant.rs:190.
-            v[i] = (float)((int)((w >> (8 * i)) & 0xFu) - 8) * d;
-            v[4 + i] = (float)((int)((w >> (8 * i + 4)) & 0xFu) - 8) * d;
+            // sign-extend the nibble to (q - 8) exactly, then one fp32 multiply, as quant.rs:190
+            v[i] = (float)((int)(w << (28 - 8 * i)) >> 28) * d;
+            v[4 + i] = (float)((int)(w << (24 - 8 * i)) >> 28) * d;
         }
     } else {
-        const uint2 w = reinterpret_cast<const uint2*>(codes + e * 32)[j];
+        const uint2 w = reinterpret_cast<const uint2*>(chunk + e * 32)[j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             v[i] = (float)(int8_t)(w.x >> (8 * i)) * d;
@@ -159,10 +166,10 @@ hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
     const dim3 grid(grid_for(nblocks, kTile));
     if (w.type == OPENMINI_QMM_Q4_0)
         hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
-                           w.groups, aligned, w.codes, w.scales);
+                           w.groups, aligned, w.chunks);
     else
         hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
-                           w.groups, aligned, w.codes, w.scales);
+                           w.groups, aligned, w.chunks);
     return hipGetLastError();
 }
 
@@ -171,11 +178,11 @@ hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s) {
     if (nwords == 0) return hipSuccess;
     const dim3 grid(grid_for(nwords, 256));
     if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(dequant_weight_kernel<true>, grid, dim3(256), 0, s, w.codes, w.scales,
-                           nwords, w.nb, w.groups, out);
+        hipLaunchKernelGGL(dequant_weight_kernel<true>, grid, dim3(256), 0, s, w.chunks, nwords,
+                           w.nb, w.groups, out);
     else
-        hipLaunchKernelGGL(dequant_weight_kernel<false>, grid, dim3(256), 0, s, w.codes, w.scales,
-                           nwords, w.nb, w.groups, out);
+        hipLaunchKernelGGL(dequant_weight_kernel<false>, grid, dim3(256), 0, s, w.chunks, nwords,
+                           w.nb, w.groups, out);
     return hipGetLastError();
 }
 
