@@ -43,10 +43,22 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+EAGER = False  # --eager: launch directly instead of from a graph (counter-collection runs)
+
+
 def time_steps(launch, steps: int, stream, hipr) -> float:
     """Wall time (ms) of `steps` back-to-back launches replayed from one HIP graph
     (captured once, so host launch cost is not what is measured), between events
     on `stream`, with the device synchronised on both sides."""
+    if EAGER:
+        hipr.hip().hipDeviceSynchronize()
+        e0, e1 = hipr.Event(), hipr.Event()
+        e0.record(stream)
+        for i in range(steps):
+            launch(i)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1)
     graph = hipr.Graph(stream, lambda s: [launch(i) for i in range(steps)])
     graph.launch(stream)  # untimed replay
     hipr.hip().hipDeviceSynchronize()
@@ -131,6 +143,32 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
     }
 
 
+def copy_calibration(qmm, hipr, stream, reps: int = 5, nbytes: int = 256 << 20) -> dict:
+    """A plain streaming copy of `nbytes` (openmini_qmm_stream_copy), the yardstick the
+    FETCH_SIZE / WRITE_SIZE counters are scaled by: it reads and writes exactly
+    `nbytes` each per launch."""
+    src, dst = qmm.DeviceBuffer(nbytes), qmm.DeviceBuffer(nbytes)
+    src.fill(1)
+    ms = time_steps(lambda i: qmm.stream_copy(dst, src, nbytes, stream.handle), reps, stream.handle, hipr)
+    src.free()
+    dst.free()
+    return {"bytes": nbytes, "launches": reps, "gbs_read_plus_write": 2 * nbytes * reps / (ms * 1e-3) / 1e9}
+
+
+def committed_traffic(workload: str):
+    """HBM bytes per launch of the GEMV kernel from the committed rocprofv3 counter
+    summary profiles/<workload>_traffic.md (FETCH_SIZE + WRITE_SIZE, each scaled by
+    the same counter's reading for the calibration copy kernel), or None."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip()), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def cpu_baseline(gemv: dict, seconds: float) -> dict:
     """The reference's per-token CPU path, restated in oracle/ (kind "port"): f32 GEMV
     over weights dequantized once at load (quant_loader.rs:76-92, model.rs:1050-1064,
@@ -197,7 +235,13 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch directly instead of replaying a HIP graph (for counter runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run the streaming-copy yardstick kernel (for counter runs)")
     args = ap.parse_args(argv)
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build targets a single MI355X and runs no "
               f"collectives (asked for --gpus {args.gpus})", file=sys.stderr)
@@ -220,9 +264,15 @@ def main(argv=None) -> int:
         gemm = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
         log(f"q8_0 gemm M=512: wall {gemm['tflops_wall']:.1f} TFLOP/s, kernel "
             f"{gemm['tflops_kernel']:.1f} TFLOP/s")
+    copy = None
+    if args.calibrate_copy:
+        copy = copy_calibration(qmm, hipr, stream)
+        log(f"stream copy {copy['bytes']} B: {copy['gbs_read_plus_write']:.1f} GB/s read+write")
     cpu = None if args.no_cpu else cpu_baseline(g, args.cpu_seconds)
 
     achieved = g["gbs_kernel"]
+    workload = "q4_0_gemv_n11008_k4096_b1"
+    traffic, traffic_src = committed_traffic(workload)
     out = {
         "metric": METRIC,
         "value": round(g["gbs_wall"], 2),
@@ -235,20 +285,23 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "arith": "int8 MFMA on 3-digit block-floating activations (int32-exact per block), fp32 accumulation",
         "data": "synthetic",
-        "config": {"workload": "q4_0_gemv_n11008_k4096_b1", "N": g["N"], "K": g["K"], "batch": 1,
+        "config": {"workload": workload, "N": g["N"], "K": g["K"], "batch": 1,
                    "weight": "Q4_0 from N(0, 0.02)", "x": "f32 N(0, 1)",
                    "weight_copies": g["weight_copies"], "rotated_bytes": g["rotated_bytes"],
                    "alg_bytes_per_step": g["alg_bytes_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel_us": round(g["kernel_ms"] * 1e3, 3)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "kernel_us": round(g["kernel_ms"] * 1e3, 3)},
         "pct_of_hbm_peak_wall": round(100.0 * g["gbs_wall"] / HBM_PEAK_GBS, 2),
         "down_proj": {"workload": "q4_0_gemv_n4096_k11008_b1", "value": round(down["gbs_wall"], 2),
                       "unit": "GB/s", "kernel_gbs": round(down["gbs_kernel"], 2),
                       "kernel_us": round(down["kernel_ms"] * 1e3, 3)},
         "cpu_baseline": cpu,
     }
+    if copy:
+        out["copy_calibration"] = copy
     if gemm:
         out["gemm"] = {
             "metric": "Q8_0 GEMM TFLOP/s M=512", "workload": "q8_0_gemm_n11008_k4096_m512_bf16x",

@@ -245,25 +245,24 @@ hipError_t run(const Weight& w, const float* x, float* y, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Phase length: one phase when the slice has at most 4 groups; 8-group phases (one
-// batch row only, for LDS) otherwise.
-template <bool kQ4, int B, int W>
-hipError_t run_p(const Weight& w, const float* x, float* y, hipStream_t s) {
-    if constexpr (B == 1) {
-        if ((w.groups + W - 1) / W > 4) return run<kQ4, B, W, 8>(w, x, y, s);
-    }
-    return run<kQ4, B, W, 4>(w, x, y, s);
-}
-
-// K slices per row tile: the most (a power of two, up to 16 for one batch row and 8
-// otherwise) that leaves each wave at least 4 groups.
+// K slices per row tile (phases of 4 groups).  One batch row: W = 8 or 16, whichever
+// pads the last phases with fewer groups (ties: 16, more waves); measured on MI355X,
+// e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  More batch rows: at most 8 (LDS and
+// registers per wave grow with the batch).  Short K: the most slices that keep 4
+// groups per wave.
 template <bool kQ4, int B>
 hipError_t run_w(const Weight& w, const float* x, float* y, hipStream_t s) {
-    if (B == 1 && w.groups >= 64) return run_p<kQ4, B, (B == 1 ? 16 : 8)>(w, x, y, s);
-    if (w.groups >= 32) return run_p<kQ4, B, 8>(w, x, y, s);
-    if (w.groups >= 16) return run_p<kQ4, B, 4>(w, x, y, s);
-    if (w.groups >= 8) return run_p<kQ4, B, 2>(w, x, y, s);
-    return run_p<kQ4, B, 1>(w, x, y, s);
+    const int64_t g = w.groups;
+    if (g >= 32) {
+        if constexpr (B == 1) {
+            const int64_t pad16 = (g + 63) / 64 * 64 - g, pad8 = (g + 31) / 32 * 32 - g;
+            if (pad16 <= pad8) return run<kQ4, B, 16, 4>(w, x, y, s);
+        }
+        return run<kQ4, B, 8, 4>(w, x, y, s);
+    }
+    if (g >= 16) return run<kQ4, B, 4, 4>(w, x, y, s);
+    if (g >= 8) return run<kQ4, B, 2, 4>(w, x, y, s);
+    return run<kQ4, B, 1, 4>(w, x, y, s);
 }
 
 template <bool kQ4>

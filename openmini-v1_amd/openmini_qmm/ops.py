@@ -132,6 +132,13 @@ class Stream:
             pass
 
 
+def stream_copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int, stream=None) -> None:
+    """The streaming-copy yardstick kernel (openmini_qmm_stream_copy): `nbytes` read and
+    written once, the reference reading for HBM traffic counters."""
+    assert nbytes <= src.nbytes and nbytes <= dst.nbytes
+    check(lib().openmini_qmm_stream_copy(dst.ptr, src.ptr, nbytes, stream))
+
+
 def init(device: int = 0) -> None:
     check(lib().openmini_qmm_init(device))
 
