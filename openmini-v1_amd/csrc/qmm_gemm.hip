@@ -7,14 +7,23 @@
 // v_mfma_f32_16x16x32_bf16 covers exactly one 32-element block, so every block's
 // partial sum is scaled by its fp32 scale and added to an fp32 accumulator:
 //   y[m, n] = sum_b d[n, b] * (sum_{k in b} x[m, k] * q[n, k]).
-// Weights are never rounded (no bf16 q*d), activations are not requantized.
+// Weights are never rounded (no bf16 q*d), activations are not requantized.  The
+// per-block rescale costs 4 VALU FMAs per MFMA, about as many VALU cycles as the
+// MFMA takes, so the kernel keeps both busy: two waves per SIMD, MFMA results in
+// VGPRs, and each MFMA issued before the FMAs of the previous one.
 //
-// Tiling: a 256-thread workgroup computes a 128 x 128 tile of y; its four waves
-// each own 64 x 64 (4 x 4 MFMA subtiles).  A K step is one 4-block group (128
-// elements): the workgroup stages X[128][128] bf16 (rows padded against bank
-// conflicts) and the group's eight 16-row weight tiles -- contiguous 1 KB / 2 KB
-// runs of the tiled layout -- in LDS; each wave converts its B fragments from the
-// LDS codes.
+// Tiling: a 512-thread workgroup computes a 128 x 192 tile of y (12 weight tiles).
+// Its 8 waves are 4 column slices x 2 K halves; a wave owns 128 rows x 48 columns
+// (3 weight tiles: 8 x 3 MFMA subtiles, 96 fp32 accumulators per lane) over one
+// half of K, and the two halves are added through LDS at the end (fixed order).
+// A K step is one 4-block group (128 elements):
+//   * x: each K half's 128 x 128 bf16 slab is copied HBM -> LDS by buffer loads
+//     with an LDS destination (no registers), double-buffered, rows XOR-swizzled in
+//     16-byte segments so the A-fragment reads are bank-conflict free;
+//   * weights: each wave loads its 3 chunks' codes and scales straight into
+//     registers two K steps ahead (three register sets: first-touch weights come
+//     from HBM, whose latency under load exceeds one step) and converts its own B
+//     fragments (its columns are its own, so nothing is converted twice).
 #include "qmm_internal.hpp"
 
 namespace qmm {
@@ -23,12 +32,9 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;                       // 8 weight tiles
-constexpr int kNT = kBN / kTileRows;
-constexpr int kKStep = kTileBlocks * kQK;      // 128 elements per LDS stage
-constexpr int kXRowBytes = kKStep * 2 + 16;    // 272: padded bf16 row
-constexpr int kThreads = 256;
+constexpr int kBM = 128;  // x rows per workgroup
+constexpr int kWT = 3;    // weight tiles (16 columns each) per wave
+constexpr int kMI = kBM / 16;  // MFMA row subtiles per wave
 
 __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     // bf16 of exactly-representable values = high halves of their fp32 bits.
@@ -65,128 +71,266 @@ __device__ __forceinline__ bf16x8 cvt_q8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<uint4*>(p));
 }
 
-template <bool kQ4>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const uint16_t* __restrict__ x,
-                                                        const uint8_t* __restrict__ chunks,
-                                                        float* __restrict__ y, int m_rows,
-                                                        int n_rows, int n_tiles, int groups, int k) {
-    constexpr int kCB = kQ4 ? 16 : 32;             // code bytes per slot
-    constexpr int kTileBytes = kTileEntries * kCB;  // codes of a chunk: 1 KB / 2 KB
+// Raw buffer resource (gfx9 descriptor): out-of-range loads return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// A wave's weight operands for one K step: per weight tile j and block tt of the
+// step, the lane's 8 codes (two words Q8_0 / one word Q4_0) and its column's scale.
+template <bool kQ4, int kSB>
+struct BRegs {
+    uint32_t c[kWT][kSB][kQ4 ? 1 : 2];
+    uint32_t s[kWT][kSB];
+};
+
+// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
+constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+
+// Workgroup shape: kNW column slices x kKS K parts of waves; a K step is kSB blocks.
+template <int kNW, int kKS, int kSB>
+struct Shape {
+    static constexpr int kThreads = 64 * kNW * kKS;
+    static constexpr int kBT = kNW * kWT;                 // weight tiles per workgroup
+    static constexpr int kRowB = kSB * kQK * 2;            // bytes of one x row per step
+    static constexpr int kSegs = kRowB / 16;               // 16-byte segments per row
+    static constexpr int kSlabB = kBM * kRowB;             // one K part's x slab per step
+    static constexpr int kStageB = kKS * kSlabB;
+    static constexpr int kRowsPerCopy = 1024 / kRowB;      // one 1 KB copy instruction
+    static constexpr int kCopies = kSlabB / kNW / 1024;     // copies per wave per step
+    static constexpr int kRedB = (kKS - 1) * kNW * kMI * kWT * 4 * 64 * 4;  // K-part partials
+    static constexpr int kLdsB = 2 * kStageB > kRedB ? 2 * kStageB : kRedB;
+    static_assert(kTileBlocks % kSB == 0, "a step covers whole blocks of one group");
+};
+
+template <bool kQ4, int kNW, int kKS, int kSB>
+__global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ chunks, float* __restrict__ y,
+    int m_rows, int n_rows, int n_tiles, int groups, int k) {
+    using S = Shape<kNW, kKS, kSB>;
+    constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kChunk = chunk_bytes_for(kQ4);
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kBM * kXRowBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t cs[kNT * kTileBytes];
-    __shared__ float ds[kNT][kTileEntries];
+    constexpr int kStepsPerGroup = kTileBlocks / kSB;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLdsB];
 
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * kBM;
-    const int tile0 = blockIdx.x * kNT;
-    const int li = lane & 15;   // row of A / column of B inside a 16 x 16 subtile
-    const int lk = lane >> 4;   // which 8-element k group of the 32-element block
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kh = wave / kNW, wn = wave % kNW;
+    const int li = lane & 15;  // A row / B column inside a 16 x 16 subtile
+    const int kq = lane >> 4;  // which 8-element quarter of the 32-element block
+    const int bx = blockIdx.x, by = blockIdx.y;
+    const int m0 = by * kBM;
+    const int tile0 = bx * S::kBT + wn * kWT;
 
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // this K part's steps; all parts step together (barriers), a shorter one idles
+    const int units = groups * kStepsPerGroup;
+    const int u0 = (int)((int64_t)units * kh / kKS);
+    const int u1 = (int)((int64_t)units * (kh + 1) / kKS);
+    const int steps = (units + kKS - 1) / kKS;
 
-    for (int g = 0; g < groups; ++g) {
-        // ---- stage X[128][128] bf16: 8 x 16 B per thread -------------------------------
+    // x is < 2 GiB (the launcher splits m); the chunks < 4 GiB (checked at upload)
+    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x, (uint32_t)m_rows * (uint32_t)k * 2u);
+    const __amdgpu_buffer_rsrc_t w_rs = make_rsrc(chunks, (uint32_t)n_tiles * groups * kChunk);
+
+    // ---- x slab copies: kCopies x 1 KB per wave per step, kRowsPerCopy rows each.
+    // LDS position p of row r holds the row's 16-byte segment s = p ^ (r % kSegs).
+    // Offsets are recomputed per copy (registers are the scarce resource here).
+    const int r_lane = wn * (kBM / kNW) + lane / S::kSegs;
+    const int p_lane = lane % S::kSegs;
+    auto issue_x = [&](int u, int stage) {
+        uint8_t* base = lds + stage * S::kStageB + kh * S::kSlabB + wn * S::kCopies * 1024;
+        const uint32_t kk0 = (uint32_t)u * (kSB * kQK);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int q = t + i * kThreads;        // 16-byte piece: row q / 16, piece q % 16
-            const int r = q >> 4, p = q & 15;
-            const int gm = min(m0 + r, m_rows - 1);
-            const int kk = g * kKStep + p * 8;     // first element of the piece
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (kk < k) v = *reinterpret_cast<const uint4*>(x + (size_t)gm * k + kk);
-            *reinterpret_cast<uint4*>(xs + r * kXRowBytes + p * 16) = v;
+        for (int j = 0; j < S::kCopies; ++j) {
+            const int r = r_lane + j * S::kRowsPerCopy;
+            const uint32_t seg = (uint32_t)((p_lane ^ (r % S::kSegs)) * 8) + kk0;
+            const uint32_t gm = (uint32_t)min(m0 + r, m_rows - 1);  // rows past m repeat the last one
+            // segments past K read zero (an out-of-range buffer offset)
+            const uint32_t voff = seg < (uint32_t)k ? (gm * (uint32_t)k + seg) * 2u : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                x_rs, (__attribute__((address_space(3))) void*)(base + j * 1024), 16, voff, 0, 0, 0);
         }
-        // ---- stage the group's 8 weight tiles and their scales -------------------------
-#pragma unroll
-        for (int i = 0; i < kNT * kTileBytes / 16 / kThreads; ++i) {
-            const int q = t + i * kThreads;        // 16-byte piece of the 8 tiles
-            const int tl = q / (kTileBytes / 16), p = q % (kTileBytes / 16);
-            const int64_t tile = min(tile0 + tl, n_tiles - 1);
-            const uint4* src = reinterpret_cast<const uint4*>(chunks + (tile * groups + g) * kChunk);
-            reinterpret_cast<uint4*>(cs)[q] = src[p];
-        }
-        for (int q = t; q < kNT * kTileEntries; q += kThreads) {
-            const int tl = q / kTileEntries, e = q % kTileEntries;
-            const int64_t tile = min(tile0 + tl, n_tiles - 1);
-            const uint16_t* sc = reinterpret_cast<const uint16_t*>(chunks + (tile * groups + g) * kChunk + kTileBytes);
-            float d = f16_bits_to_f32(sc[e]);
-            if constexpr (kQ4) d *= 16.0f;
-            ds[tl][e] = d;
-        }
-        __syncthreads();
+    };
 
+    // ---- weight operands: chunk (tile j, group g), slot (t, li), quarter kq
+    uint32_t tile_off[kWT];
 #pragma unroll
-        for (int bt = 0; bt < kTileBlocks; ++bt) {  // block slot within the group
-            bf16x8 a[4], bfr[4];
-            float dsc[4];
+    for (int j = 0; j < kWT; ++j) tile_off[j] = (uint32_t)min(tile0 + j, n_tiles - 1) * groups * kChunk;
+    auto load_b = [&](BRegs<kQ4, kSB>& B, int u) {
+        const int g = u / kStepsPerGroup, t0 = (u % kStepsPerGroup) * kSB;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm * 64 + i * 16 + li;
-                a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
-                                                      xs + r * kXRowBytes + (bt * kQK + lk * 8) * 2));
-            }
+        for (int j = 0; j < kWT; ++j) {
+            const uint32_t soff = tile_off[j] + (uint32_t)g * kChunk;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int tl = wn * 4 + j;                 // the 16 columns are one weight tile
-                const int e = bt * kTileRows + li;         // entry (block slot bt, row li)
-                const uint8_t* cp = cs + tl * kTileBytes + e * kCB;
+            for (int tt = 0; tt < kSB; ++tt) {
+                const uint32_t slot = (uint32_t)((t0 + tt) * kTileRows + li);
+                B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, kTileEntries * kCB + slot * 2, soff, 0);
                 if constexpr (kQ4) {
-                    bfr[j] = cvt_q4(*reinterpret_cast<const uint32_t*>(cp + lk * 4));
+                    B.c[j][tt][0] = __builtin_amdgcn_raw_buffer_load_b32(w_rs, slot * kCB + kq * 4, soff, 0);
                 } else {
-                    const uint32_t* c32 = reinterpret_cast<const uint32_t*>(cp + lk * 8);
-                    bfr[j] = cvt_q8(c32[0], c32[1]);
+                    const uint2 v = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(w_rs, slot * kCB + kq * 8, soff, 0));
+                    B.c[j][tt][0] = v.x;
+                    B.c[j][tt][1] = v.y;
                 }
-                dsc[j] = ds[tl][e];
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a[i], bfr[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[r], dsc[j], acc[i][j][r]);
-                }
         }
-        __syncthreads();
-    }
+    };
 
-    // ---- store: lane holds D[4*lk + r][li] of each subtile ---------------------------
+    f32x4 acc[kMI][kWT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kMI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int gn = (tile0 + wn * 4 + j) * kTileRows + li;
-            if (gn >= n_rows) continue;
+        for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // One step of this wave's work from LDS stage `stage` and weight registers `B`.
+    auto compute = [&](const BRegs<kQ4, kSB>& B, int stage) {
+        const uint8_t* slab = lds + stage * S::kStageB + kh * S::kSlabB;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int gm = m0 + wm * 64 + i * 16 + lk * 4 + r;
-                if (gm < m_rows) y[(size_t)gm * n_rows + gn] = acc[i][j][r];
+        for (int tt = 0; tt < kSB; ++tt) {
+            bf16x8 b[kWT];
+            float d[kWT];
+#pragma unroll
+            for (int j = 0; j < kWT; ++j) {
+                const uint16_t dh = (uint16_t)B.s[j][tt];
+                if constexpr (kQ4) {
+                    b[j] = cvt_q4(B.c[j][tt][0]);
+                    d[j] = f16_bits_to_f32(dh) * 16.0f;
+                } else {
+                    b[j] = cvt_q8(B.c[j][tt][0], B.c[j][tt][1]);
+                    d[j] = f16_bits_to_f32(dh);
+                }
+            }
+            bf16x8 a[kMI];
+#pragma unroll
+            for (int i = 0; i < kMI; ++i) {
+                const int r = i * 16 + li;
+                a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                      slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16)));
+            }
+            // MFMA q + 1 is issued before the FMAs of q (two result registers)
+            f32x4 pp[2];
+            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kMI * kWT; ++q) {
+                if (q + 1 < kMI * kWT)
+                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a[(q + 1) / kWT], b[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
             }
         }
+    };
+
+    // Step `it` (unit u = u0 + it): the x copies for u were issued one step earlier,
+    // the weights for u two steps earlier.  Per step the wave issues x(u + 1), then
+    // the weights of u + 2 (kBLoads loads), so waiting until at most kBLoads loads
+    // are outstanding completes x(u) and everything older; one barrier then makes
+    // every wave's copies visible and frees the other x stage.  The loads are
+    // unconditional (units past this part's end re-load its last unit, a cache hit)
+    // so the count of outstanding loads is the same on every path; the compiler's
+    // own waits before the barrier then cover only the x copies.
+    constexpr int kBLoads = kWT * kSB * 2;
+    const int u_last = max(u1 - 1, 0);
+    auto step = [&](int it, const BRegs<kQ4, kSB>& cur, BRegs<kQ4, kSB>& far) {
+        const int u = u0 + it;
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
+        __syncthreads();
+        issue_x(min(u + 1, u_last), (it + 1) & 1);
+        asm volatile("" ::: "memory");  // keep the weight loads after the copies (vmcnt order)
+        load_b(far, min(u + 2, u_last));
+        if (u < u1) compute(cur, it & 1);  // uniform per wave
+    };
+
+    BRegs<kQ4, kSB> b0, b1, b2;
+    issue_x(min(u0, u_last), 0);
+    asm volatile("" ::: "memory");
+    load_b(b0, min(u0, u_last));
+    load_b(b1, min(u0 + 1, u_last));
+    int it = 0;
+    for (; it + 2 < steps; it += 3) {  // three register sets rotate: no copies
+        step(it, b0, b2);
+        step(it + 1, b1, b0);
+        step(it + 2, b2, b1);
+    }
+    if (it < steps) step(it, b0, b2);
+    if (it + 1 < steps) step(it + 1, b1, b0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no copy may land after the stages are reused
+
+    // ---- K parts meet in LDS (the stages are free after this barrier), then store.
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(lds);
+    constexpr int kAcc = kMI * kWT * 4;  // accumulators per lane
+    if (kh > 0) {
+        float* mine = red + ((size_t)(kh - 1) * kNW + wn) * kAcc * 64;
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+#pragma unroll
+            for (int j = 0; j < kWT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mine[((i * kWT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kh == 0) {
+        const bool full_m = m0 + kBM <= m_rows;
+#pragma unroll
+        for (int j = 0; j < kWT; ++j) {
+            const int gn = (tile0 + j) * kTileRows + li;
+            if (tile0 + j >= n_tiles || gn >= n_rows) continue;
+            float* yc = y + gn;
+#pragma unroll
+            for (int i = 0; i < kMI; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    // lane holds D[4 kq + r][li] of each 16 x 16 subtile; parts added in order
+                    float v = acc[i][j][r];
+#pragma unroll
+                    for (int h = 1; h < kKS; ++h)
+                        v += red[(((size_t)(h - 1) * kNW + wn) * kAcc + (i * kWT + j) * 4 + r) * 64 + lane];
+                    const int gm = m0 + i * 16 + kq * 4 + r;
+                    if (full_m || gm < m_rows) yc[(size_t)gm * n_rows] = v;
+                }
+        }
+    }
+}
+
+template <bool kQ4, int kNW, int kKS, int kSB>
+hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
+    using S = Shape<kNW, kKS, kSB>;
+    const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
+    hipLaunchKernelGGL((gemm_kernel<kQ4, kNW, kKS, kSB>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
+                       (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+    return hipGetLastError();
+}
+
+// Shape by the number of 128-row blocks of x: one -> 1 column slice x 4 K parts
+// (tile 128 x 48, one workgroup per CU), more -> 2 column slices x 2 K halves (tile
+// 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers overlap the other's
+// work).  Measured on MI355X against 4 x 2 (128 x 192) with 2- and 4-block K steps:
+// equal or faster on Q8_0 11008 x 4096 at M = 128 / 512 / 2048.
+template <bool kQ4>
+hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
+    if (m <= kBM) return launch_shape<kQ4, 1, 4, 2>(w, x, y, m, s);
+    return launch_shape<kQ4, 2, 2, 2>(w, x, y, m, s);
 }
 
 }  // namespace
 
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m,
                             hipStream_t s) {
-    if (m <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((w.n_tiles + kNT - 1) / kNT), (unsigned)((m + kBM - 1) / kBM));
-    if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(kThreads), 0, s, x, w.chunks, y, (int)m,
-                           (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
-    else
-        hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(kThreads), 0, s, x, w.chunks, y, (int)m,
-                           (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
-    return hipGetLastError();
+    // x offsets are 32-bit: launches cover row ranges whose x is below 2 GiB.
+    const int64_t rows_per_launch = ((((int64_t)1 << 31) - 1) / (w.k * 2)) / kBM * kBM;
+    if (rows_per_launch <= 0) return hipErrorInvalidValue;  // one row tile of x exceeds 2 GiB
+    for (int64_t m_off = 0; m_off < m; m_off += rows_per_launch) {
+        const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
+        const uint16_t* xs = x + m_off * w.k;
+        float* ys = y + m_off * w.n;
+        const hipError_t e = w.type == OPENMINI_QMM_Q4_0 ? launch_kind<true>(w, xs, ys, mm, s)
+                                                         : launch_kind<false>(w, xs, ys, mm, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace qmm
