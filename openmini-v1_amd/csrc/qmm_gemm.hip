@@ -183,43 +183,44 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
 #pragma unroll
         for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // One step of this wave's work from LDS stage `stage` and weight registers `B`.
-    auto compute = [&](const BRegs<kQ4, kSB>& B, int stage) {
+    // A fragments of block tt of the step in LDS stage `stage`: rows i * 16 + li,
+    // elements 8 kq .. 8 kq + 7 of the block (swizzled segment).
+    typedef bf16x8 AFrags[kMI];
+    auto read_a = [&](AFrags& a, int stage, int tt) {
         const uint8_t* slab = lds + stage * S::kStageB + kh * S::kSlabB;
 #pragma unroll
-        for (int tt = 0; tt < kSB; ++tt) {
-            bf16x8 b[kWT];
-            float d[kWT];
+        for (int i = 0; i < kMI; ++i) {
+            const int r = i * 16 + li;
+            a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                  slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16)));
+        }
+    };
+    // Block tt of one step: 8 x 3 MFMAs on A fragments `a` and the weight registers.
+    auto compute = [&](const BRegs<kQ4, kSB>& B, const AFrags& a, int tt) {
+        bf16x8 b[kWT];
+        float d[kWT];
 #pragma unroll
-            for (int j = 0; j < kWT; ++j) {
-                const uint16_t dh = (uint16_t)B.s[j][tt];
-                if constexpr (kQ4) {
-                    b[j] = cvt_q4(B.c[j][tt][0]);
-                    d[j] = f16_bits_to_f32(dh) * 16.0f;
-                } else {
-                    b[j] = cvt_q8(B.c[j][tt][0], B.c[j][tt][1]);
-                    d[j] = f16_bits_to_f32(dh);
-                }
+        for (int j = 0; j < kWT; ++j) {
+            const uint16_t dh = (uint16_t)B.s[j][tt];
+            if constexpr (kQ4) {
+                b[j] = cvt_q4(B.c[j][tt][0]);
+                d[j] = f16_bits_to_f32(dh) * 16.0f;
+            } else {
+                b[j] = cvt_q8(B.c[j][tt][0], B.c[j][tt][1]);
+                d[j] = f16_bits_to_f32(dh);
             }
-            bf16x8 a[kMI];
+        }
+        // MFMA q + 1 is issued before the FMAs of q (two result registers)
+        f32x4 pp[2];
+        pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < kMI; ++i) {
-                const int r = i * 16 + li;
-                a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
-                                                      slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16)));
-            }
-            // MFMA q + 1 is issued before the FMAs of q (two result registers)
-            f32x4 pp[2];
-            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        for (int q = 0; q < kMI * kWT; ++q) {
+            if (q + 1 < kMI * kWT)
+                pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    a[(q + 1) / kWT], b[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int q = 0; q < kMI * kWT; ++q) {
-                if (q + 1 < kMI * kWT)
-                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        a[(q + 1) / kWT], b[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
-            }
+            for (int r = 0; r < 4; ++r)
+                acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
         }
     };
 
@@ -238,9 +239,26 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
         __syncthreads();
         issue_x(min(u + 1, u_last), (it + 1) & 1);
-        asm volatile("" ::: "memory");  // keep the weight loads after the copies (vmcnt order)
+        // The weight loads go between the step's blocks: issued right after the copies,
+        // every wave of the CU would queue its vector-memory instructions at once and
+        // stall its MFMAs behind them.  The memory clobbers keep the issue order (the
+        // copies before the weights) that the vmcnt count above relies on.
+        asm volatile("" ::: "memory");
+        const bool live = u < u1;  // uniform per wave
+        AFrags a;
+        if (live) {
+            read_a(a, it & 1, 0);
+            compute(cur, a, 0);
+        }
+        asm volatile("" ::: "memory");
         load_b(far, min(u + 2, u_last));
-        if (u < u1) compute(cur, it & 1);  // uniform per wave
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tt = 1; tt < kSB; ++tt)
+            if (live) {
+                read_a(a, it & 1, tt);
+                compute(cur, a, tt);
+            }
     };
 
     BRegs<kQ4, kSB> b0, b1, b2;
