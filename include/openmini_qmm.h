@@ -53,10 +53,20 @@ typedef enum {
     OPENMINI_QMM_ERR_INSUFFICIENT_DATA = -11 /* QuantError::InsufficientData{expected, actual} */
 } openmini_qmm_status_t;
 
-/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240). */
+/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload, GEMV and
+ * GEMM take Q4_0 and Q8_0; the dequantization entry points take every id listed. */
 typedef enum {
+    OPENMINI_QMM_F32 = 0,
+    OPENMINI_QMM_F16 = 1,
     OPENMINI_QMM_Q4_0 = 2,
-    OPENMINI_QMM_Q8_0 = 7
+    OPENMINI_QMM_Q4_1 = 3,
+    OPENMINI_QMM_Q8_0 = 7,
+    OPENMINI_QMM_Q2_K = 10,
+    OPENMINI_QMM_Q3_K = 11,
+    OPENMINI_QMM_Q4_K = 12,
+    OPENMINI_QMM_Q5_K = 13,
+    OPENMINI_QMM_Q6_K = 14,
+    OPENMINI_QMM_Q8_K = 15
 } openmini_qmm_type_t;
 
 /* A quantized weight W[n_rows, k_cols] resident in HBM in the GPU layout. */
@@ -93,7 +103,8 @@ int openmini_qmm_is_available(void);
 int openmini_qmm_device_info(char* buf, size_t buf_len);
 
 /* GgufTensor::data_size (src/model/inference/gguf.rs:431-438):
- * ceil(n_elements / 32) * bytes_per_block.  Pure host computation. */
+ * ceil(n_elements / block_size) * bytes_per_block for every type id above.  Pure host
+ * computation. */
 int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes);
 
 /* GpuQuantOps::estimate_memory_usage (quant_simd.rs:2985): device bytes a
@@ -150,10 +161,11 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
  * Bit-identical to quant::dequantize of the original GGUF bytes. */
 int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, void* stream);
 
-/* quant_simd::safe_dequantize semantics (quant_simd.rs:150-241, 284-302) on raw
- * GGUF bytes in device memory: n == 0 -> OK (nothing written); gguf_bytes <
- * ceil(n/32)*bpb -> INSUFFICIENT_DATA with *expected_bytes set; other types ->
- * UNSUPPORTED.  Writes n floats. expected_bytes may be NULL. */
+/* quant_simd::safe_dequantize semantics (quant_simd.rs:150-302) on raw GGUF bytes in
+ * device memory, for Q4_0, Q8_0 and Q4_1: n == 0 -> OK (nothing written); gguf_bytes
+ * < ceil(n/32)*bpb -> INSUFFICIENT_DATA with *expected_bytes set; other types ->
+ * UNSUPPORTED (QuantError::UnsupportedType).  Writes n floats.  expected_bytes may be
+ * NULL. */
 int openmini_qmm_dequantize_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n,
                                    float* d_out, void* stream, size_t* expected_bytes);
 
@@ -161,6 +173,19 @@ int openmini_qmm_dequantize_device(int type, const void* d_gguf, size_t gguf_byt
  * host bytes in, host floats out, synchronous, same validation as above. */
 int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_t n,
                             float* out, size_t* expected_bytes);
+
+/* quant::dequantize semantics (src/model/inference/quant.rs:56-79), the CPU path that
+ * GpuQuantOps::batch_dequantize_gpu falls back to (quant_simd.rs:3104-3118 via
+ * dequantize_simd :304-313), for F32, F16, Q4_0, Q4_1, Q8_0 and Q2_K..Q8_K: the blocks
+ * that fit in gguf_bytes are dequantized, the rest of the n outputs are 0.0 (the
+ * reference stops at the first incomplete block).  Bit-identical to the reference,
+ * signed zeros included.  Other type ids -> UNSUPPORTED (the reference returns zeros
+ * for types it does not implement; the IQ types are not implemented here). */
+int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n,
+                                       float* d_out, void* stream);
+
+/* Same on host memory, synchronous. */
+int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out);
 
 /* ---- device memory and streams for callers without a HIP binding of their own ----- */
 

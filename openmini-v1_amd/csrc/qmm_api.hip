@@ -4,6 +4,7 @@
 // message for openmini_qmm_last_error(); nothing aborts.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -46,7 +47,15 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
+// Weight layouts (upload, GEMV, GEMM).
 bool type_supported(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
+// quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
+bool safe_type(int type) { return type_supported(type) || type == OPENMINI_QMM_Q4_1; }
+// ceil(n / block_size) * bytes_per_block (gguf.rs:431-438); 0 for unknown types.
+size_t layout_bytes(int type, size_t n) {
+    const int bs = qmm::layout_block_size(type);
+    return bs ? (n + bs - 1) / bs * (size_t)qmm::layout_bytes_per_block(type) : 0;
+}
 
 // Device probing is done once per device; the result is cached.
 std::mutex g_dev_mu;
@@ -196,14 +205,14 @@ int openmini_qmm_device_info(char* buf, size_t buf_len) {
 
 int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes) {
     if (!out_bytes) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_bytes");
-    if (!type_supported(type)) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
-    *out_bytes = (n_elements + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    if (!qmm::layout_block_size(type)) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
+    *out_bytes = layout_bytes(type, n_elements);
     return ok();
 }
 
 size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements) {
-    const size_t bpb = type_supported(type) ? (size_t)qmm::bytes_per_block(type) : 4u * qmm::kQK;
-    return (n_elements + qmm::kQK - 1) / qmm::kQK * bpb + n_elements * sizeof(float);
+    const size_t in = qmm::layout_block_size(type) ? layout_bytes(type, n_elements) : n_elements * sizeof(float);
+    return in + n_elements * sizeof(float);
 }
 
 int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes, int64_t n_rows,
@@ -356,9 +365,9 @@ int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, 
 
 static int validate_dequant(int type, size_t gguf_bytes, size_t n, size_t* expected_bytes) {
     if (expected_bytes) *expected_bytes = 0;
-    if (!type_supported(type))
+    if (!safe_type(type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "UnsupportedType(%d)", type);
-    const size_t need = (n + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    const size_t need = layout_bytes(type, n);
     if (gguf_bytes < need) {
         if (expected_bytes) *expected_bytes = need;
         return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA, "InsufficientData: expected %zu bytes, actual %zu",
@@ -375,8 +384,8 @@ int openmini_qmm_dequantize_device(int type, const void* d_gguf, size_t gguf_byt
     if (!d_gguf || !d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
     rc = ensure_device(nullptr);
     if (rc != OPENMINI_QMM_OK) return rc;
-    hipError_t e = qmm::launch_dequant_gguf(type, static_cast<const uint8_t*>(d_gguf), n, d_out,
-                                            as_stream(stream));
+    hipError_t e = qmm::launch_dequant_layout(type, static_cast<const uint8_t*>(d_gguf), gguf_bytes, n, d_out,
+                                              as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
     return ok();
 }
@@ -389,7 +398,7 @@ int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_
     if (!gguf || !out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
     rc = ensure_device(nullptr);
     if (rc != OPENMINI_QMM_OK) return rc;
-    const size_t need = (n + qmm::kQK - 1) / qmm::kQK * (size_t)qmm::bytes_per_block(type);
+    const size_t need = layout_bytes(type, n);
     void *din = nullptr, *dout = nullptr;
     hipError_t e = hipMalloc(&din, need);
     if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(float));
@@ -399,8 +408,49 @@ int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_
     }
     e = hipMemcpy(din, gguf, need, hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = qmm::launch_dequant_gguf(type, static_cast<const uint8_t*>(din), n, static_cast<float*>(dout),
-                                     nullptr);
+        e = qmm::launch_dequant_layout(type, static_cast<const uint8_t*>(din), need, n, static_cast<float*>(dout),
+                                       nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(din);
+    (void)hipFree(dout);
+    if (e != hipSuccess) return hip_fail(e, "dequantize");
+    return ok();
+}
+
+int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n, float* d_out,
+                                       void* stream) {
+    if (!qmm::layout_block_size(type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "tensor type %d is not implemented", type);
+    if (n == 0) return ok();
+    if (!d_out || (!d_gguf && gguf_bytes)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t used = std::min(gguf_bytes, layout_bytes(type, n));
+    hipError_t e = qmm::launch_dequant_layout(type, static_cast<const uint8_t*>(d_gguf), used, n, d_out,
+                                              as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return ok();
+}
+
+int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out) {
+    if (!qmm::layout_block_size(type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "tensor type %d is not implemented", type);
+    if (n == 0) return ok();
+    if (!out || (!gguf && gguf_bytes)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t used = std::min(gguf_bytes, layout_bytes(type, n));
+    void *din = nullptr, *dout = nullptr;
+    hipError_t e = hipMalloc(&din, used ? used : 1);
+    if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipFree(din);
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for dequantize failed: %s", hipGetErrorString(e));
+    }
+    if (used) e = hipMemcpy(din, gguf, used, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = qmm::launch_dequant_layout(type, static_cast<const uint8_t*>(din), used, n, static_cast<float*>(dout),
+                                       nullptr);
     if (e == hipSuccess) e = hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost);
     (void)hipFree(din);
     (void)hipFree(dout);

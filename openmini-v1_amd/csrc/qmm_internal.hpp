@@ -47,6 +47,34 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 inline int bytes_per_block(int type) {
     return type == OPENMINI_QMM_Q4_0 ? 18 : type == OPENMINI_QMM_Q8_0 ? 34 : 0;
 }
+
+// GgufTensorType::{block_size, bytes_per_block} (src/model/inference/gguf.rs:348-379)
+// for the layouts the dequantization entry points accept; 0 for others.
+inline int layout_block_size(int type) {
+    switch (type) {
+    case OPENMINI_QMM_F32: case OPENMINI_QMM_F16: return 1;
+    case OPENMINI_QMM_Q4_0: case OPENMINI_QMM_Q4_1: case OPENMINI_QMM_Q8_0: return 32;
+    case OPENMINI_QMM_Q2_K: case OPENMINI_QMM_Q3_K: case OPENMINI_QMM_Q4_K: case OPENMINI_QMM_Q5_K:
+    case OPENMINI_QMM_Q6_K: case OPENMINI_QMM_Q8_K: return 256;
+    default: return 0;
+    }
+}
+inline int layout_bytes_per_block(int type) {
+    switch (type) {
+    case OPENMINI_QMM_F32: return 4;
+    case OPENMINI_QMM_F16: return 2;
+    case OPENMINI_QMM_Q4_0: return 18;
+    case OPENMINI_QMM_Q4_1: return 20;
+    case OPENMINI_QMM_Q8_0: return 34;
+    case OPENMINI_QMM_Q2_K: return 68;
+    case OPENMINI_QMM_Q3_K: return 162;
+    case OPENMINI_QMM_Q4_K: return 144;
+    case OPENMINI_QMM_Q5_K: return 176;
+    case OPENMINI_QMM_Q6_K: return 210;
+    case OPENMINI_QMM_Q8_K: return 258;
+    default: return 0;
+    }
+}
 inline int code_bytes_per_block(int type) {
     return type == OPENMINI_QMM_Q4_0 ? 16 : type == OPENMINI_QMM_Q8_0 ? 32 : 0;
 }
@@ -100,6 +128,12 @@ hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hip
 // y[m][n] = x_bf16[m][k] . W^T.
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m,
                             hipStream_t s);
+
+// quant::dequantize semantics for every layout the library knows (F32, F16, Q4_0,
+// Q4_1, Q8_0, Q2_K..Q8_K): complete blocks of `bytes` are dequantized, the rest of the
+// n_elems outputs are zero.  hipErrorInvalidValue for other types.
+hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, size_t n_elems, float* out,
+                                 hipStream_t s);
 
 hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 

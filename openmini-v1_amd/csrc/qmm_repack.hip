@@ -3,6 +3,8 @@
 // Reference semantics (paths relative to openmini-server/):
 //   quant::dequantize_q4_0  src/model/inference/quant.rs:152-195
 //   quant::dequantize_q8_0  src/model/inference/quant.rs:282-316
+//   quant::dequantize_{q4_1, q2_k, q3_k, q4_k, q5_k, q6_k, q8_k}, f32 / f16 arms:
+//                           quant.rs:95-133, 216-262, 338-800
 //   f16 scale decode        quant.rs:166-167, 296-297 (half::f16::to_f32, exact)
 // Q4_0 GGUF byte j of a block holds element 2j in its HIGH nibble and element
 // 2j+1 in its LOW nibble (quant.rs:179-188); value = (q - 8) * f32(d).
@@ -146,6 +148,148 @@ __global__ __launch_bounds__(256) void dequant_gguf_kernel(const uint8_t* __rest
     }
 }
 
+// ---- the other GGUF layouts of quant::dequantize (quant.rs:56-79, 216-800) -----------
+//
+// One thread per 8 consecutive outputs.  Each value follows the reference's formula
+// with one IEEE operation per Rust operator, in its order, and no contraction: every
+// product in these formulas is exact in binary32 (at most 23 significant bits), so
+// only the final additions round and the results are bit-identical, signed zeros
+// included.  Blocks past `avail_blocks` (short input) produce zeros, as the reference
+// stops at the first block that does not fit (e.g. quant.rs:224-226).
+
+__device__ __forceinline__ float f16_at(const uint8_t* p) {
+    return f16_bits_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+}
+
+// quant.rs:216-262: [d][m][16 B codes]; element 2j high nibble, 2j+1 low; q * d + m.
+__device__ float elem_q4_1(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b), m = f16_at(b + 2);
+    const uint8_t c = b[4 + i / 2];
+    const float q = (float)((i & 1) ? (c & 0x0F) : (c >> 4));
+    return q * d + m;
+}
+// quant.rs:338-410: the minimum is read past the 8 scale bytes, so it is 0.0.
+__device__ float elem_q4_k(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b), dmin = f16_at(b + 2);
+    const int sb = i >> 5, j = i & 31;
+    const float scale = (float)(b[4 + sb] & 0x3F);
+    const uint8_t c = b[12 + sb * 16 + j / 2];
+    const float q = (float)((j & 1) ? (c & 0x0F) : (c >> 4));
+    const float t = (q - 8.0f) * d * scale;
+    return t + dmin * 0.0f;
+}
+// quant.rs:433-505
+__device__ float elem_q5_k(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b), dmin = f16_at(b + 2);
+    const int sb = i >> 5, j = i & 31;
+    const float scale = (float)(b[4 + sb] & 0x3F);
+    const uint8_t mb = b[4 + 8 + sb / 2];
+    const float min_val = (float)((sb & 1) ? (mb >> 4) : (mb & 0x0F));
+    const float qh_bit = (float)((b[20 + sb] >> (j & 7)) & 1);
+    const uint8_t c = b[36 + sb * 16 + j / 2];
+    const float q4 = (float)((j & 1) ? (c & 0x0F) : (c >> 4));
+    const float q = q4 + qh_bit * 16.0f;
+    const float t = (q - 16.0f) * d * scale;
+    return t + dmin * min_val;
+}
+// quant.rs:515-600
+__device__ float elem_q6_k(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b);
+    const float scale = (float)(int8_t)b[130 + i / 16];
+    const uint8_t l = b[2 + i / 2];
+    const int low = (i & 1) ? (l >> 4) : (l & 0x0F);
+    const int high = (b[66 + i / 4] >> ((i & 3) * 2)) & 0x03;
+    const int q = low | ((high << 4) - 32);
+    return (float)q * d * scale;
+}
+// quant.rs:605-660: code bytes past the 32 of the block give q = 1 (:645-649).
+__device__ float elem_q2_k(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b), dmin = f16_at(b + 2);
+    const int sb = i >> 4, j = i & 15;
+    const float scale = (float)b[4 + sb], min_val = (float)b[20 + sb];
+    const int byte_idx = sb * 8 + j / 4;
+    const float q = byte_idx < 32 ? (float)((b[36 + byte_idx] >> ((j & 3) * 2)) & 0x03) : 1.0f;
+    const float t = (q - 2.0f) * d * scale;
+    return t + dmin * min_val;
+}
+// quant.rs:682-760
+__device__ float elem_q3_k(const uint8_t* b, int i) {
+#pragma clang fp contract(off)
+    const float d = f16_at(b);
+    const float scale = (float)(int8_t)b[130 + i / 8];
+    const uint8_t l = b[2 + i / 2];
+    const int lb = (i & 1) ? ((l >> 4) & 0x07) : (l & 0x07);
+    const int hb = (b[66 + i / 4] >> ((i & 3) * 2)) & 0x01;
+    const int q = (lb | (hb << 3)) - 16;
+    return (float)q * d * scale;
+}
+// quant.rs:768-800
+__device__ float elem_q8_k(const uint8_t* b, int i) { return (float)(int8_t)b[2 + i] * f16_at(b); }
+// quant.rs:152-195, 282-316
+__device__ float elem_q4_0(const uint8_t* b, int i) { return (float)((int)q4_code(b + 2, i) - 8) * f16_at(b); }
+__device__ float elem_q8_0(const uint8_t* b, int i) { return (float)(int8_t)b[2 + i] * f16_at(b); }
+
+template <int kType>
+struct Layout;
+template <> struct Layout<OPENMINI_QMM_Q4_0> { static constexpr int kQ = 32, kB = 18; };
+template <> struct Layout<OPENMINI_QMM_Q8_0> { static constexpr int kQ = 32, kB = 34; };
+template <> struct Layout<OPENMINI_QMM_Q4_1> { static constexpr int kQ = 32, kB = 20; };
+template <> struct Layout<OPENMINI_QMM_Q2_K> { static constexpr int kQ = 256, kB = 68; };
+template <> struct Layout<OPENMINI_QMM_Q3_K> { static constexpr int kQ = 256, kB = 162; };
+template <> struct Layout<OPENMINI_QMM_Q4_K> { static constexpr int kQ = 256, kB = 144; };
+template <> struct Layout<OPENMINI_QMM_Q5_K> { static constexpr int kQ = 256, kB = 176; };
+template <> struct Layout<OPENMINI_QMM_Q6_K> { static constexpr int kQ = 256, kB = 210; };
+template <> struct Layout<OPENMINI_QMM_Q8_K> { static constexpr int kQ = 256, kB = 258; };
+
+template <int kType>
+__device__ __forceinline__ float elem(const uint8_t* b, int i) {
+    if constexpr (kType == OPENMINI_QMM_Q4_0) return elem_q4_0(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q8_0) return elem_q8_0(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q4_1) return elem_q4_1(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q2_K) return elem_q2_k(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q3_K) return elem_q3_k(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q4_K) return elem_q4_k(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q5_K) return elem_q5_k(b, i);
+    if constexpr (kType == OPENMINI_QMM_Q6_K) return elem_q6_k(b, i);
+    return elem_q8_k(b, i);
+}
+
+template <int kType>
+__global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __restrict__ gguf, size_t n,
+                                                             size_t avail_blocks, float* __restrict__ out) {
+    using L = Layout<kType>;
+    const size_t e0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (e0 >= n) return;
+    const size_t blk = e0 / L::kQ;
+    const int i0 = (int)(e0 % L::kQ);
+    const uint8_t* b = gguf + blk * L::kB;
+    const bool have = blk < avail_blocks;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if (e0 + j < n) out[e0 + j] = have ? elem<kType>(b, i0 + j) : 0.0f;
+}
+
+// F32 / F16 arms (quant.rs:95-133): element-wise, missing bytes give 0.
+__global__ __launch_bounds__(256) void dequant_plain_kernel(const uint8_t* __restrict__ src, size_t n,
+                                                            size_t avail, int f16, float* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (i >= avail) {
+        out[i] = 0.0f;
+    } else if (f16) {
+        out[i] = f16_at(src + 2 * i);
+    } else {
+        uint32_t v = (uint32_t)src[4 * i] | ((uint32_t)src[4 * i + 1] << 8) | ((uint32_t)src[4 * i + 2] << 16) |
+                     ((uint32_t)src[4 * i + 3] << 24);
+        out[i] = __uint_as_float(v);
+    }
+}
+
 __global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restrict__ src,
                                                           uint4* __restrict__ dst, int64_t n16) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -196,6 +340,37 @@ hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, fl
     else
         hipLaunchKernelGGL(dequant_gguf_kernel<34>, grid, dim3(256), 0, s, gguf, n_elems, out);
     return hipGetLastError();
+}
+
+hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, size_t n_elems, float* out,
+                                 hipStream_t s) {
+    if (n_elems == 0) return hipSuccess;
+    if (type == OPENMINI_QMM_F32 || type == OPENMINI_QMM_F16) {
+        const size_t esz = type == OPENMINI_QMM_F16 ? 2 : 4;
+        hipLaunchKernelGGL(dequant_plain_kernel, dim3(grid_for((int64_t)n_elems, 256)), dim3(256), 0, s, gguf, n_elems,
+                           bytes / esz, type == OPENMINI_QMM_F16 ? 1 : 0, out);
+        return hipGetLastError();
+    }
+    const dim3 grid(grid_for((int64_t)((n_elems + 7) / 8), 256));
+    switch (type) {
+#define QMM_LAYOUT_CASE(T)                                                                              \
+    case T:                                                                                             \
+        hipLaunchKernelGGL(dequant_layout_kernel<T>, grid, dim3(256), 0, s, gguf, n_elems,              \
+                           bytes / Layout<T>::kB, out);                                                 \
+        return hipGetLastError();
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q4_0)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q8_0)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q4_1)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q2_K)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q3_K)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q4_K)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q5_K)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q6_K)
+        QMM_LAYOUT_CASE(OPENMINI_QMM_Q8_K)
+#undef QMM_LAYOUT_CASE
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s) {

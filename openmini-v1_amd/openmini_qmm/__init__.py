@@ -7,5 +7,6 @@ operator interface (see ops.py) plus synthetic-input helpers (synth.py).
 from ._native import LIB_PATH, Q4_0, Q8_0, QmmError, lib  # noqa: F401
 from .ops import (DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,  # noqa: F401
                   InsufficientData, InvalidInput, QuantError, QuantizedWeight, Stream,
-                  UnsupportedType, get_gemm_engine, init, linear, linear_gemm, safe_dequantize,
-                  safe_dequantize_q4_0, safe_dequantize_q8_0, stream_copy)
+                  UnsupportedType, dequantize, dequantize_simd, get_gemm_engine, init, linear,
+                  linear_gemm, safe_dequantize, safe_dequantize_q4_0, safe_dequantize_q4_1,
+                  safe_dequantize_q8_0, stream_copy)

@@ -60,6 +60,8 @@ SIGNATURES = {
     "openmini_qmm_dequant_weight": (_i, [_p, _p, _p]),
     "openmini_qmm_dequantize_device": (_i, [_i, _p, _sz, _sz, _p, _p, ctypes.POINTER(_sz)]),
     "openmini_qmm_dequantize": (_i, [_i, _p, _sz, _sz, _p, ctypes.POINTER(_sz)]),
+    "openmini_qmm_dequantize_any_device": (_i, [_i, _p, _sz, _sz, _p, _p]),
+    "openmini_qmm_dequantize_any": (_i, [_i, _p, _sz, _sz, _p]),
     "openmini_qmm_malloc": (_i, [ctypes.POINTER(_p), _sz]),
     "openmini_qmm_free": (_i, [_p]),
     "openmini_qmm_memcpy_h2d": (_i, [_p, _p, _sz, _p]),

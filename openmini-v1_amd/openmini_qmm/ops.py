@@ -3,7 +3,8 @@ HIP C-ABI.  Names, argument meaning and error behaviour follow the reference
 (paths relative to openmini-server/):
 
   QuantError / InsufficientData / UnsupportedType   quant_simd.rs:91-103
-  safe_dequantize{,_q4_0,_q8_0}                     quant_simd.rs:150-241, 284-302
+  safe_dequantize{,_q4_0,_q8_0,_q4_1}               quant_simd.rs:150-302
+  dequantize / dequantize_simd                      quant.rs:56-79, quant_simd.rs:304-313
   GpuQuantOps -> HipQuantOps                        quant_simd.rs:2944-2986 (trait),
                                                     :3137-3188 (the CUDA stub it replaces)
   GemmEngine -> HipQuantGemmEngine                  model/inference/gemm_engine.rs:37-56
@@ -26,18 +27,26 @@ QK = 32
 
 
 class GgufTensorType(enum.IntEnum):
-    """GGUF type ids, model/inference/gguf.rs:219-240 (the subset this path handles,
-    plus F32/F16 so callers can ask for them and get UnsupportedType)."""
+    """GGUF type ids, model/inference/gguf.rs:219-240: the layouts this library
+    dequantizes (weights for the GEMV/GEMM: Q4_0 and Q8_0)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
+    Q4_1 = 3
     Q8_0 = 7
+    Q2K = 10
+    Q3K = 11
+    Q4K = 12
+    Q5K = 13
+    Q6K = 14
+    Q8K = 15
 
     def bytes_per_block(self) -> int:  # gguf.rs:356-379
-        return {0: 4, 1: 2, 2: 18, 7: 34}[int(self)]
+        return {0: 4, 1: 2, 2: 18, 3: 20, 7: 34, 10: 68, 11: 162, 12: 144, 13: 176, 14: 210,
+                15: 258}[int(self)]
 
     def block_size(self) -> int:  # gguf.rs:327-338
-        return {0: 1, 1: 1, 2: 32, 7: 32}[int(self)]
+        return 1 if int(self) < 2 else 32 if int(self) < 10 else 256
 
 
 # ---- quant_simd::QuantError --------------------------------------------------------
@@ -203,11 +212,33 @@ class QuantizedWeight:
 
 # ---- quant_simd safe API (validated dequantization) on the GPU ----------------------
 
+def dequantize(data, tensor_type, n: int) -> np.ndarray:
+    """quant::dequantize (quant.rs:56-79), which dequantize_simd (quant_simd.rs:304-313)
+    matches value for value: the blocks that fit in `data` are dequantized, the rest
+    of the n outputs are 0.0; bit-identical to the reference.  Types the library does
+    not implement raise UnsupportedType (the reference returns zeros)."""
+    tt = int(tensor_type)
+    buf = _as_u8(data)
+    out = np.empty(max(int(n), 0), dtype=np.float32)
+    rc = lib().openmini_qmm_dequantize_any(tt, _ptr(buf), buf.size, int(n), _ptr(out) if n else None)
+    if rc == _native.ERR_UNSUPPORTED:
+        raise UnsupportedType(tensor_type)
+    check(rc)
+    return out
+
+
+dequantize_simd = dequantize
+
+
 def safe_dequantize(data, tensor_type, n: int) -> np.ndarray:
     """quant_simd::safe_dequantize (quant_simd.rs:284-302): n == 0 -> empty;
-    short input -> InsufficientData{expected, actual}; other types -> UnsupportedType."""
+    Q4_0 / Q8_0 / Q4_1: short input -> InsufficientData{expected, actual};
+    F16 / F32: dequantize_simd without a length check (:293-299); other types ->
+    UnsupportedType."""
     tt = int(tensor_type)
-    if tt not in (GgufTensorType.Q4_0, GgufTensorType.Q8_0):
+    if tt in (GgufTensorType.F16, GgufTensorType.F32):
+        return dequantize(data, tt, n)
+    if tt not in (GgufTensorType.Q4_0, GgufTensorType.Q8_0, GgufTensorType.Q4_1):
         raise UnsupportedType(tensor_type)
     buf = _as_u8(data)
     out = np.empty(max(int(n), 0), dtype=np.float32)
@@ -230,12 +261,19 @@ def safe_dequantize_q8_0(data, n: int) -> np.ndarray:
     return safe_dequantize(data, GgufTensorType.Q8_0, n)
 
 
+def safe_dequantize_q4_1(data, n: int) -> np.ndarray:
+    return safe_dequantize(data, GgufTensorType.Q4_1, n)
+
+
 # ---- GpuQuantOps ----------------------------------------------------------------------
 
 class HipQuantOps:
     """HIP implementation of trait GpuQuantOps (quant_simd.rs:2944-2986), in place of
     the CudaQuantOps stub (:3137-3188).  Rust's Result<Vec<f32>, String> maps to a
-    returned array or a raised GpuQuantOpsError carrying the string."""
+    returned array or a raised GpuQuantOpsError carrying the string.  The per-type
+    calls validate their input like safe_dequantize (a short buffer is an error);
+    batch_dequantize_gpu takes any implemented type with dequantize_simd's semantics,
+    as the reference's working implementation does (MetalQuantOps, :3104-3118)."""
 
     class GpuQuantOpsError(RuntimeError):
         pass
@@ -253,10 +291,13 @@ class HipQuantOps:
         return self._deq(GgufTensorType.Q8_0, data, n)
 
     def dequantize_q4_1_gpu(self, data, n: int) -> np.ndarray:
-        raise HipQuantOps.GpuQuantOpsError("Q4_1 is not implemented by the HIP backend")
+        return self._deq(GgufTensorType.Q4_1, data, n)
 
     def batch_dequantize_gpu(self, tensors) -> list:
-        return [self._deq(t, d, n) for (t, d, n) in tensors]
+        try:
+            return [dequantize(d, t, n) for (t, d, n) in tensors]
+        except (QuantError, QmmError) as e:
+            raise HipQuantOps.GpuQuantOpsError(str(e)) from e
 
     def is_available(self) -> bool:
         return bool(lib().openmini_qmm_is_available())

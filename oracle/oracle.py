@@ -16,9 +16,13 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libqmm_oracle.so")
 
-F32, F16, Q4_0, Q8_0 = 0, 1, 2, 7
+F32, F16, Q4_0, Q4_1, Q8_0 = 0, 1, 2, 3, 7
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 10, 11, 12, 13, 14, 15
 QK = 32
-BYTES_PER_BLOCK = {Q4_0: 18, Q8_0: 34}
+BYTES_PER_BLOCK = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q2_K: 68, Q3_K: 162, Q4_K: 144, Q5_K: 176,
+                   Q6_K: 210, Q8_K: 258}
+BLOCK_SIZE = {Q4_0: 32, Q4_1: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256,
+              Q6_K: 256, Q8_K: 256}
 
 _lib = None
 
@@ -46,7 +50,7 @@ def lib():
             "orc_data_size": (sz, [i, sz]),
             "orc_dequantize_q4_0": (None, [p, sz, sz, p]),
             "orc_dequantize_q8_0": (None, [p, sz, sz, p]),
-            "orc_dequantize": (None, [i, p, sz, sz, p]),
+            "orc_dequantize": (i, [i, p, sz, sz, p]),
             "orc_safe_dequantize": (i, [i, p, sz, sz, p, ctypes.POINTER(sz)]),
             "orc_convert_to_soa": (sz, [i, p, sz, sz, p]),
             "orc_quantize_q4_0": (None, [p, sz, p]),
@@ -118,6 +122,12 @@ def safe_dequantize(qtype: int, data, n: int):
     return st, (out[:n] if st == 0 else None), exp.value
 
 
+def restated(qtype: int) -> bool:
+    """Whether quant::dequantize's arm for `qtype` is restated in the oracle."""
+    out = np.empty(1, dtype=np.float32)
+    return bool(lib().orc_dequantize(qtype, None, 0, 0, _ptr(out)))
+
+
 def convert_to_soa(qtype: int, data, n: int) -> np.ndarray:
     d = _u8(data)
     blocks = (n + QK - 1) // QK
@@ -183,6 +193,21 @@ def create_test_q4_0_data(n: int) -> np.ndarray:
     for i in range(blocks):
         h = f32_to_f16(np.float32(0.1) + np.float32(i) * np.float32(0.01))
         out += bytes([h & 0xFF, h >> 8])
+        for j in range(16):
+            v = (i * 16 + j) % 16
+            out.append(((v << 4) | (v & 0x0F)) & 0xFF)
+    return np.frombuffer(bytes(out), dtype=np.uint8).copy()
+
+
+def create_test_q4_1_data(n: int) -> np.ndarray:
+    """tests/quant_simd_regression_test.rs:72-94: d_i = f16(0.15 + 0.015 i),
+    m_i = f16(-1.0 + 0.1 i), byte j = v << 4 | v with v = (16 i + j) % 16."""
+    blocks = (n + QK - 1) // QK
+    out = bytearray()
+    for i in range(blocks):
+        h = f32_to_f16(np.float32(0.15) + np.float32(i) * np.float32(0.015))
+        m = f32_to_f16(np.float32(-1.0) + np.float32(i) * np.float32(0.1))
+        out += bytes([h & 0xFF, h >> 8, m & 0xFF, m >> 8])
         for j in range(16):
             v = (i * 16 + j) % 16
             out.append(((v << 4) | (v & 0x0F)) & 0xFF)

@@ -14,6 +14,9 @@
  *                           tests/quant_simd_regression_test.rs), asymmetric-nibble
  *                           KAT from quant.rs:179-190, and an independent numpy
  *                           vectorised restatement on the regression generators
+ *   orc_dequantize_q4_1/_k  reference KATs where they exist (quant.rs:1499-1610,
+ *                           2093-2130, quant_simd.rs:4270-4290), hand-computed blocks
+ *                           for every field of each layout, and a numpy restatement
  *   orc_safe_dequantize     InsufficientData payloads of the regression tests
  *   orc_convert_to_soa      quant_simd.rs KATs (lengths 72/68, first scale bytes)
  *                           plus a brute-force permutation check
@@ -107,12 +110,16 @@ float orc_bf16_to_f32(uint16_t b) {
 
 /* ---- GGUF block geometry (src/model/inference/gguf.rs:327-379, 424-438) ---- */
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 7 };
+enum {
+    ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q8_0 = 7,
+    ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_Q8_K = 15
+};
 
 size_t orc_block_size(int type) {
     switch (type) {
     case ORC_F32: case ORC_F16: return 1;
-    case ORC_Q4_0: case ORC_Q8_0: return 32;
+    case ORC_Q4_0: case ORC_Q4_1: case ORC_Q8_0: return 32;
+    case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_Q8_K: return 256;
     default: return 0;
     }
 }
@@ -122,7 +129,14 @@ size_t orc_bytes_per_block(int type) {
     case ORC_F32: return 4;
     case ORC_F16: return 2;
     case ORC_Q4_0: return 18;
+    case ORC_Q4_1: return 20;
     case ORC_Q8_0: return 34;
+    case ORC_Q2_K: return 68;
+    case ORC_Q3_K: return 162;
+    case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
+    case ORC_Q6_K: return 210;
+    case ORC_Q8_K: return 258;
     default: return 0;
     }
 }
@@ -177,35 +191,232 @@ void orc_dequantize_q8_0(const uint8_t *data, size_t len, size_t n, float *out) 
     }
 }
 
-/* quant::dequantize dispatcher restricted to the path's types, quant.rs:56-79
- * (F32 via dequantize_f32, F16 via dequantize_f16; other types -> zeros :78). */
-void orc_dequantize(int type, const uint8_t *data, size_t len, size_t n, float *out) {
+static float f16_at(const uint8_t *p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* Every formula below is evaluated in the reference's order with one IEEE operation per
+ * Rust operator (Rust does not contract a * b + c).  All its products are exact in
+ * binary32, so only the final additions round. */
+
+/* quant::dequantize_q4_1, quant.rs:216-262: 20-byte blocks [d f16][m f16][16 B codes];
+ * element 2j = high nibble of byte j, 2j+1 = low nibble; value = q * d + m. */
+void orc_dequantize_q4_1(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + QK - 1) / QK;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 20;
+        if (off + 20 > len) break;
+        float d = f16_at(data + off), m = f16_at(data + off + 2);
+        const uint8_t *qs = data + off + 4;
+        for (size_t i = 0; i < QK; ++i) {
+            size_t idx = b * QK + i;
+            if (idx >= n) break;
+            float q = (float)((i % 2 == 0) ? (qs[i / 2] >> 4) : (qs[i / 2] & 0x0F));
+            float prod = q * d;
+            out[idx] = prod + m;
+        }
+    }
+}
+
+/* quant::dequantize_q4_k, quant.rs:338-410: 144-byte blocks [d][dmin][scales 8 B]
+ * [codes from byte 12]; 8 sub-blocks of 32; scale = scales[sb] & 0x3F; the minimum is
+ * read from scales[8 + sb / 2], past the 8-byte slice, so it is 0.0 (:360-378);
+ * value = (q - 8) * d * scale + dmin * min. */
+void orc_dequantize_q4_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 144;
+        if (off + 144 > len) break;
+        const uint8_t *blk = data + off;
+        float d = f16_at(blk), dmin = f16_at(blk + 2);
+        const uint8_t *scales = blk + 4, *qs = blk + 12;
+        for (int sb = 0; sb < 8; ++sb) {
+            float scale = (float)(scales[sb] & 0x3F);
+            float min_val = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                size_t idx = b * 256 + (size_t)sb * 32 + (size_t)i;
+                if (idx >= n) break;
+                uint8_t byte = qs[sb * 16 + i / 2];
+                float q = (float)((i % 2 == 0) ? (byte >> 4) : (byte & 0x0F));
+                float t = (q - 8.0f) * d;
+                t = t * scale;
+                float u = dmin * min_val;
+                out[idx] = t + u;
+            }
+        }
+    }
+}
+
+/* quant::dequantize_q5_k, quant.rs:433-505: 176-byte blocks [d][dmin][scales 16 B]
+ * [qh 16 B][codes from byte 36]; scale = scales[sb] & 0x3F, min = nibble (sb even: low,
+ * odd: high) of scales[8 + sb / 2]; q = nibble + 16 * bit (i % 8) of qh[sb];
+ * value = (q - 16) * d * scale + dmin * min. */
+void orc_dequantize_q5_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 176;
+        if (off + 176 > len) break;
+        const uint8_t *blk = data + off;
+        float d = f16_at(blk), dmin = f16_at(blk + 2);
+        const uint8_t *scales = blk + 4, *qh = blk + 20, *qs = blk + 36;
+        for (int sb = 0; sb < 8; ++sb) {
+            float scale = (float)(scales[sb] & 0x3F);
+            uint8_t mb = scales[8 + sb / 2];
+            float min_val = (float)((sb % 2 == 0) ? (mb & 0x0F) : (mb >> 4));
+            for (int i = 0; i < 32; ++i) {
+                size_t idx = b * 256 + (size_t)sb * 32 + (size_t)i;
+                if (idx >= n) break;
+                float qh_bit = (float)((qh[sb] >> (i % 8)) & 1);
+                uint8_t byte = qs[sb * 16 + i / 2];
+                float q4 = (float)((i % 2 == 0) ? (byte >> 4) : (byte & 0x0F));
+                float hi = qh_bit * 16.0f;
+                float q = q4 + hi;
+                float t = (q - 16.0f) * d;
+                t = t * scale;
+                float u = dmin * min_val;
+                out[idx] = t + u;
+            }
+        }
+    }
+}
+
+/* quant::dequantize_q6_k, quant.rs:515-600: 210-byte blocks [d][ql 64 B][qh 64 B]
+ * [scales 32 x i8]; element i: low = nibble of ql[i / 2] (even i: low, odd: high),
+ * high = 2 bits (i % 4) of qh[i / 4]; q = low | ((high << 4) - 32);
+ * value = q * d * scales[i / 16]. */
+void orc_dequantize_q6_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 210;
+        if (off + 210 > len) break;
+        const uint8_t *blk = data + off;
+        float d = f16_at(blk);
+        const uint8_t *ql = blk + 2, *qh = blk + 66, *scales = blk + 130;
+        for (int i = 0; i < 256; ++i) {
+            size_t idx = b * 256 + (size_t)i;
+            if (idx >= n) break;
+            float scale = (float)(int8_t)scales[i / 16];
+            int low = (i % 2 == 0) ? (ql[i / 2] & 0x0F) : (ql[i / 2] >> 4);
+            int high = (qh[i / 4] >> ((i % 4) * 2)) & 0x03;
+            int q = low | ((high << 4) - 32);
+            float t = (float)q * d;
+            out[idx] = t * scale;
+        }
+    }
+}
+
+/* quant::dequantize_q2_k, quant.rs:605-660: 68-byte blocks [d][dmin][scales 16 x u8]
+ * [mins 16 x u8][codes 32 B]; 16 sub-blocks of 16; code byte sb * 8 + i / 4 (past the
+ * 32 code bytes from sub-block 4 on: q = 1, :645-649), 2 bits (i % 4);
+ * value = (q - 2) * d * scale + dmin * min. */
+void orc_dequantize_q2_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 68;
+        if (off + 68 > len) break;
+        const uint8_t *blk = data + off;
+        float d = f16_at(blk), dmin = f16_at(blk + 2);
+        const uint8_t *scales = blk + 4, *mins = blk + 20, *qs = blk + 36;
+        for (int sb = 0; sb < 16; ++sb) {
+            float scale = (float)scales[sb], min_val = (float)mins[sb];
+            for (int i = 0; i < 16; ++i) {
+                size_t idx = b * 256 + (size_t)sb * 16 + (size_t)i;
+                if (idx >= n) break;
+                int byte_idx = sb * 8 + i / 4;
+                float q = byte_idx < 32 ? (float)((qs[byte_idx] >> ((i % 4) * 2)) & 0x03) : 1.0f;
+                float t = (q - 2.0f) * d;
+                t = t * scale;
+                float u = dmin * min_val;
+                out[idx] = t + u;
+            }
+        }
+    }
+}
+
+/* quant::dequantize_q3_k, quant.rs:682-760: 162-byte blocks [d][ql 64 B][qh 64 B]
+ * [scales 32 x i8]; element i: 3 bits (even i: bits 0-2, odd: bits 4-6) of ql[i / 2],
+ * bit 2 (i % 4) of qh[i / 4] as bit 3; q = that - 16; value = q * d * scales[i / 8]. */
+void orc_dequantize_q3_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 162;
+        if (off + 162 > len) break;
+        const uint8_t *blk = data + off;
+        float d = f16_at(blk);
+        const uint8_t *ql = blk + 2, *qh = blk + 66, *scales = blk + 130;
+        for (int i = 0; i < 256; ++i) {
+            size_t idx = b * 256 + (size_t)i;
+            if (idx >= n) break;
+            float scale = (float)(int8_t)scales[i / 8];
+            int lb = (i % 2 == 0) ? (ql[i / 2] & 0x07) : ((ql[i / 2] >> 4) & 0x07);
+            int hb = (qh[i / 4] >> ((i % 4) * 2)) & 0x01;
+            int q = (lb | (hb << 3)) - 16;
+            float t = (float)q * d;
+            out[idx] = t * scale;
+        }
+    }
+}
+
+/* quant::dequantize_q8_k, quant.rs:768-800: 258-byte blocks [d][256 x i8];
+ * value = q * d. */
+void orc_dequantize_q8_k(const uint8_t *data, size_t len, size_t n, float *out) {
+    size_t blocks = (n + 255) / 256;
+    for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+    for (size_t b = 0; b < blocks; ++b) {
+        size_t off = b * 258;
+        if (off + 258 > len) break;
+        float d = f16_at(data + off);
+        const uint8_t *qs = data + off + 2;
+        for (int i = 0; i < 256; ++i) {
+            size_t idx = b * 256 + (size_t)i;
+            if (idx >= n) break;
+            out[idx] = (float)(int8_t)qs[i] * d;
+        }
+    }
+}
+
+/* quant::dequantize dispatcher, quant.rs:56-79 (F32 via dequantize_f32, F16 via
+ * dequantize_f16; the IQ types are not restated here; other types -> zeros :78).
+ * Returns 1 for a type restated here, 0 otherwise (output zeroed). */
+int orc_dequantize(int type, const uint8_t *data, size_t len, size_t n, float *out) {
     switch (type) {
-    case ORC_Q4_0: orc_dequantize_q4_0(data, len, n, out); return;
-    case ORC_Q8_0: orc_dequantize_q8_0(data, len, n, out); return;
+    case ORC_Q4_0: orc_dequantize_q4_0(data, len, n, out); return 1;
+    case ORC_Q4_1: orc_dequantize_q4_1(data, len, n, out); return 1;
+    case ORC_Q8_0: orc_dequantize_q8_0(data, len, n, out); return 1;
+    case ORC_Q2_K: orc_dequantize_q2_k(data, len, n, out); return 1;
+    case ORC_Q3_K: orc_dequantize_q3_k(data, len, n, out); return 1;
+    case ORC_Q4_K: orc_dequantize_q4_k(data, len, n, out); return 1;
+    case ORC_Q5_K: orc_dequantize_q5_k(data, len, n, out); return 1;
+    case ORC_Q6_K: orc_dequantize_q6_k(data, len, n, out); return 1;
+    case ORC_Q8_K: orc_dequantize_q8_k(data, len, n, out); return 1;
     case ORC_F32:
         for (size_t i = 0; i < n; ++i) {
             if (4 * i + 4 <= len) memcpy(&out[i], data + 4 * i, 4); else out[i] = 0.0f;
         }
-        return;
+        return 1;
     case ORC_F16:
         for (size_t i = 0; i < n; ++i) {
             out[i] = (2 * i + 2 <= len)
                 ? orc_f16_to_f32((uint16_t)(data[2 * i] | (data[2 * i + 1] << 8))) : 0.0f;
         }
-        return;
+        return 1;
     default:
         for (size_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return 0;
     }
 }
 
-/* quant_simd::safe_dequantize{,_q4_0,_q8_0}, quant_simd.rs:150-241 and :284-302.
+/* quant_simd::safe_dequantize{,_q4_0,_q8_0,_q4_1}, quant_simd.rs:150-302.
  * Returns 0 = Ok, 1 = InsufficientData{expected=*expected, actual=len},
  * 2 = UnsupportedType.  n == 0 -> Ok with empty output. */
 int orc_safe_dequantize(int type, const uint8_t *data, size_t len, size_t n, float *out,
                         size_t *expected) {
     if (expected) *expected = 0;
-    if (type != ORC_Q4_0 && type != ORC_Q8_0) return 2;
+    if (type != ORC_Q4_0 && type != ORC_Q8_0 && type != ORC_Q4_1) return 2;
     if (n == 0) return 0;
     size_t need = orc_data_size(type, n);
     if (len < need) {

@@ -40,7 +40,11 @@ def test_host_only_validation():
     assert L.openmini_qmm_required_bytes(2, 4096 * 11008, ctypes.byref(out)) == 0
     assert out.value == 25_362_432
     assert L.openmini_qmm_required_bytes(7, 33, ctypes.byref(out)) == 0 and out.value == 68
-    assert L.openmini_qmm_required_bytes(10, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
+    # every layout the dequantization entry points take (gguf.rs:348-379, 431-438)
+    for t, n, want in ((3, 33, 40), (10, 32, 68), (11, 256, 162), (12, 257, 288), (13, 256, 176),
+                       (14, 512, 420), (15, 1, 258), (0, 3, 12), (1, 3, 6)):
+        assert L.openmini_qmm_required_bytes(t, n, ctypes.byref(out)) == 0 and out.value == want, t
+    assert L.openmini_qmm_required_bytes(16, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
     assert L.openmini_qmm_estimate_memory_usage(2, 64) == 36 + 256
 
     h = ctypes.c_void_p()
@@ -62,6 +66,12 @@ def test_host_only_validation():
     assert L.openmini_qmm_dequantize(2, p, 10, 32, p, ctypes.byref(exp)) == _native.ERR_INSUFFICIENT_DATA
     assert exp.value == 18
     assert L.openmini_qmm_dequantize(10, p, 64, 32, p, ctypes.byref(exp)) == _native.ERR_UNSUPPORTED
+    # Q4_1 is validated like Q4_0 / Q8_0: 20-byte blocks
+    assert L.openmini_qmm_dequantize(3, p, 10, 32, p, ctypes.byref(exp)) == _native.ERR_INSUFFICIENT_DATA
+    assert exp.value == 20
+    # quant::dequantize semantics: unknown layouts are refused before any device work
+    assert L.openmini_qmm_dequantize_any(16, p, 64, 256, p) == _native.ERR_UNSUPPORTED
+    assert L.openmini_qmm_dequantize_any(12, None, 0, 0, None) == 0
 
 
 def test_python_mirror_raises_reference_errors():
@@ -72,4 +82,7 @@ def test_python_mirror_raises_reference_errors():
     assert (ei.value.expected, ei.value.actual) == (18, 10)
     with pytest.raises(UnsupportedType):
         safe_dequantize(b"", 10, 32)
+    with pytest.raises(InsufficientData) as ei:
+        safe_dequantize(bytes(30), 3, 64)
+    assert (ei.value.expected, ei.value.actual) == (40, 30)
     assert safe_dequantize_q4_0(b"", 0).size == 0

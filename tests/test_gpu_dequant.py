@@ -1,7 +1,7 @@
 """GPU dequantization and upload/repack: bit-exact against the oracle.
 
-Reference semantics: quant::dequantize_q4_0 / _q8_0 (src/model/inference/quant.rs:152-195,
-282-316) and quant_simd::safe_dequantize (quant_simd.rs:150-241, 284-302).
+Reference semantics: quant::dequantize and its per-layout arms (src/model/inference/
+quant.rs:56-800) and quant_simd::safe_dequantize (quant_simd.rs:150-302).
 """
 import json
 import os
@@ -14,6 +14,13 @@ from openmini_qmm import synth
 pytestmark = pytest.mark.gpu
 Q4_0, Q8_0 = 2, 7
 BPB = {Q4_0: 18, Q8_0: 34}
+# every layout of the any-type entry point: type -> (block size, bytes per block)
+LAYOUTS = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 7: (32, 34), 10: (256, 68),
+           11: (256, 162), 12: (256, 144), 13: (256, 176), 14: (256, 210), 15: (256, 258)}
+SAFE = (2, 3, 7)
+# byte offsets of the fp16 fields (scales, minimums) inside each block
+F16_FIELDS = {2: (0,), 3: (0, 2), 7: (0,), 10: (0, 2), 11: (0,), 12: (0, 2), 13: (0, 2), 14: (0,),
+              15: (0,)}
 KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
 
 
@@ -74,19 +81,84 @@ def test_non_finite_scales_propagate(qmm, orc, qtype):
 @pytest.mark.parametrize("case", KATS["dequantize"], ids=lambda c: c["src"].split()[-1])
 def test_reference_kats_on_gpu(qmm, orc, case):
     data = bytes.fromhex(case["hex"])
-    need = (case["n"] + 31) // 32 * BPB[case["type"]]
-    if len(data) < need:
-        # quant::dequantize zero-fills; the safe GPU API reports InsufficientData
-        with pytest.raises(qmm.InsufficientData) as ei:
-            qmm.safe_dequantize(data, case["type"], case["n"])
-        assert ei.value.expected == need and ei.value.actual == len(data)
-        return
-    got = qmm.safe_dequantize(data, case["type"], case["n"])
+    t = case["type"]
+    bs, bpb = LAYOUTS[t]
+    need = (case["n"] + bs - 1) // bs * bpb
+    ref = orc.dequantize(t, data, case["n"])
+    # quant::dequantize semantics (zero tail on short input) for every layout
+    got = qmm.dequantize(data, t, case["n"])
     assert got.size == case["expect_len"]
-    assert np.array_equal(bits(got), bits(orc.dequantize(case["type"], data, case["n"])))
+    assert np.array_equal(bits(got), bits(ref))
     if "expect_prefix" in case:
         exp = np.array(case["expect_prefix"], dtype=np.float32)
         assert np.all(np.abs(got[: exp.size] - exp) <= case["tol"])
+    if "all_value" in case:
+        assert np.all(got == np.float32(case["all_value"]))
+    if t not in SAFE:
+        return
+    if len(data) < need:
+        # the safe GPU API reports InsufficientData
+        with pytest.raises(qmm.InsufficientData) as ei:
+            qmm.safe_dequantize(data, t, case["n"])
+        assert ei.value.expected == need and ei.value.actual == len(data)
+        return
+    assert np.array_equal(bits(qmm.safe_dequantize(data, t, case["n"])), bits(ref))
+
+
+def layout_bytes(qtype, nblocks, seed, finite=True):
+    bs, bpb = LAYOUTS[qtype]
+    raw = np.random.default_rng(seed).integers(0, 256, nblocks * bpb, dtype=np.uint8)
+    if finite:
+        for f in F16_FIELDS.get(qtype, ()):
+            raw[f + 1::bpb] &= 0x7B  # fp16 exponent never all-ones
+        if qtype == 1:
+            raw[1::2] &= 0x7B
+        if qtype == 0:
+            raw[3::4] &= 0x7E  # no inf / nan floats
+    return raw
+
+
+@pytest.mark.parametrize("qtype", sorted(LAYOUTS))
+def test_every_layout_random_bytes_bit_exact(qmm, orc, qtype):
+    """Random bytes in every field (scales, minimums, codes, high bits), zero scales on
+    some blocks (signed zeros), a ragged n, and a short buffer (zero tail)."""
+    bs, bpb = LAYOUTS[qtype]
+    nblk = 3000 if bs == 256 else 20000
+    raw = layout_bytes(qtype, nblk, seed=qtype + 1)
+    for f in F16_FIELDS.get(qtype, ()):  # zero d / m / dmin on the first blocks
+        for k in range(20):
+            raw[k * bpb + f: k * bpb + f + 2] = 0
+    print(f"dequantize_any type={qtype} blocks={nblk}", flush=True)
+    for n in (nblk * bs, nblk * bs - bs // 2 - 3):
+        got = qmm.dequantize(raw, qtype, n)
+        assert np.array_equal(bits(got), bits(orc.dequantize(qtype, raw, n))), n
+    short = raw[: (nblk // 2) * bpb + bpb // 3]
+    got = qmm.dequantize(short, qtype, nblk * bs)
+    ref = orc.dequantize(qtype, short, nblk * bs)
+    assert np.array_equal(bits(got), bits(ref))
+    assert np.all(got[(nblk // 2) * bs:] == 0.0)
+
+
+@pytest.mark.parametrize("qtype", [3, 10, 11, 12, 13, 14, 15])
+def test_every_layout_non_finite_scales(qmm, orc, qtype):
+    raw = layout_bytes(qtype, 64, seed=77, finite=False)
+    bpb = LAYOUTS[qtype][1]
+    for f in F16_FIELDS[qtype]:
+        raw[f + 1::bpb] |= 0x7C  # inf / nan scales and minimums
+    n = 64 * LAYOUTS[qtype][0]
+    got, ref = qmm.dequantize(raw, qtype, n), orc.dequantize(qtype, raw, n)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(bits(got[fin]), bits(ref[fin]))
+
+
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_k_quant_llama_projection_size(qmm, orc, qtype):
+    """A full 11008 x 4096 projection in the layouts real deployments use (Q4_K, Q6_K)."""
+    n = 11008 * 4096
+    raw = layout_bytes(qtype, n // 256, seed=qtype * 3)
+    got = qmm.dequantize(raw, qtype, n)
+    assert np.array_equal(bits(got), bits(orc.dequantize(qtype, raw, n)))
 
 
 @pytest.mark.parametrize("case", KATS["safe_dequantize"], ids=lambda c: c["src"].split()[1])
@@ -151,5 +223,15 @@ def test_gpu_quant_ops_mirror(qmm, orc):
     assert np.array_equal(bits(outs[1]), bits(orc.dequantize(Q8_0, data8, 256)))
     with pytest.raises(ops.GpuQuantOpsError):
         ops.dequantize_q8_0_gpu(bytes(10), 32)
+    data1 = orc.create_test_q4_1_data(256)
+    assert np.array_equal(bits(ops.dequantize_q4_1_gpu(data1, 256)), bits(orc.dequantize(3, data1, 256)))
     with pytest.raises(ops.GpuQuantOpsError):
-        ops.dequantize_q4_1_gpu(bytes(20), 32)
+        ops.dequantize_q4_1_gpu(bytes(19), 32)
+    # batch: any implemented layout, dequantize_simd semantics (short input: zero tail)
+    kq = layout_bytes(12, 4, seed=5)
+    outs = ops.batch_dequantize_gpu([(12, kq, 1024), (12, kq[:300], 1024), (14, bytes(210), 256)])
+    assert np.array_equal(bits(outs[0]), bits(orc.dequantize(12, kq, 1024)))
+    assert np.array_equal(bits(outs[1]), bits(orc.dequantize(12, kq[:300], 1024)))
+    assert np.all(outs[1][512:] == 0.0) and np.all(np.signbit(outs[2]))
+    with pytest.raises(ops.GpuQuantOpsError):
+        ops.batch_dequantize_gpu([(16, bytes(64), 256)])

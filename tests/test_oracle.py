@@ -302,3 +302,133 @@ def test_golden_regression(orc):
         N, K = g[f"{tag}_shape"]
         assert np.array_equal(orc.linear_f64(qtype, blocks, int(N), int(K), x), g[f"{tag}_y"])
         assert np.array_equal(orc.dequantize(qtype, blocks, int(N * K)), g[f"{tag}_w"])
+
+
+# ---- Q4_1 and the K-quant layouts (quant.rs:216-262, 338-800) --------------------------
+# Each block below sets every field of its layout to a distinct value and the expected
+# outputs are worked out by hand from the reference source, so a swapped nibble, a
+# wrong field offset, a dropped term or a wrong sign changes at least one of them.
+Q4_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 3, 10, 11, 12, 13, 14, 15
+
+
+def _f16(v):
+    return list(np.array([v], dtype=np.float16).view(np.uint8))
+
+
+def test_q4_1_hand_block(orc):
+    blk = bytearray(_f16(2.0) + _f16(-1.5) + [0] * 16)
+    blk[4] = 0x3A    # elements 0, 1: q = 3, 10
+    blk[19] = 0xF0   # elements 30, 31: q = 15, 0
+    out = orc.dequantize(Q4_1, bytes(blk), 32)
+    assert out[0] == 4.5 and out[1] == 18.5 and out[30] == 28.5 and out[31] == -1.5
+    assert np.all(out[2:30] == -1.5)   # q = 0: the offset alone
+
+
+def test_q4_k_hand_block_and_missing_minimum(orc):
+    blk = bytearray(144)
+    blk[0:2] = bytes(_f16(0.5))
+    blk[2:4] = bytes(_f16(3.0))        # dmin: its term vanishes (min read past scales)
+    blk[4] = 0xC5                      # sub-block 0 scale = 0xC5 & 0x3F = 5
+    blk[5] = 0x02                      # sub-block 1 scale = 2
+    blk[12] = 0x9F                     # elements 0, 1: q = 9, 15
+    blk[12 + 16] = 0x70                # elements 32, 33: q = 7, 0
+    out = orc.dequantize(Q4_K, bytes(blk), 256)
+    assert out[0] == 2.5 and out[1] == 17.5 and out[32] == -1.0 and out[33] == -8.0
+    assert out[2] == -20.0             # q = 0 in sub-block 0: (0 - 8) * 0.5 * 5
+    assert np.all(out[64:] == 0.0)     # scales 0: (q - 8) * d * 0 + 0
+
+
+def test_q5_k_hand_block(orc):
+    blk = bytearray(176)
+    blk[0:2] = bytes(_f16(1.0))
+    blk[2:4] = bytes(_f16(0.5))
+    blk[4], blk[5] = 3, 4              # scales of sub-blocks 0, 1
+    blk[4 + 8] = 0x21                  # minimums: sub-block 0 low nibble 1, 1 high nibble 2
+    blk[20] = 0b00000010               # qh of sub-block 0: bit 1 -> element 1 gets +16
+    blk[36] = 0x5A                     # elements 0, 1: nibbles 5, 10
+    blk[36 + 16] = 0x01                # elements 32, 33: nibbles 0, 1
+    out = orc.dequantize(Q5_K, bytes(blk), 256)
+    assert out[0] == (5 - 16) * 3 + 0.5 * 1          # -32.5
+    assert out[1] == (26 - 16) * 3 + 0.5 * 1         # 30.5
+    assert out[32] == (0 - 16) * 4 + 0.5 * 2         # -63
+    assert out[33] == (1 - 16) * 4 + 0.5 * 2         # -59
+
+
+def test_q6_k_hand_block(orc):
+    blk = bytearray(210)
+    blk[0:2] = bytes(_f16(0.25))
+    blk[2] = 0x2F                      # elements 0, 1: low nibbles 15 (even), 2 (odd)
+    blk[66] = 0b00011011               # high 2-bit fields of elements 0..3: 3, 2, 1, 0
+    blk[130] = 0xFE                    # scale of elements 0..15: -2
+    blk[131] = 0x03                    # scale of elements 16..31: 3
+    out = orc.dequantize(Q6_K, bytes(blk), 256)
+    assert out[0] == 31 * 0.25 * -2    # q = 15 | (48 - 32)
+    assert out[1] == 2 * 0.25 * -2     # q = 2 | (32 - 32)
+    assert out[2] == -16 * 0.25 * -2   # q = 0 | (16 - 32)
+    assert out[3] == -32 * 0.25 * -2   # q = 0 | (0 - 32)
+    assert out[16] == -32 * 0.25 * 3
+
+
+def test_q2_k_hand_block_and_short_code_array(orc):
+    blk = bytearray(68)
+    blk[0:2] = bytes(_f16(1.0))
+    blk[2:4] = bytes(_f16(0.5))
+    blk[4], blk[20] = 3, 2             # sub-block 0: scale 3, minimum 2
+    blk[4 + 4], blk[20 + 4] = 1, 0     # sub-block 4: scale 1, minimum 0
+    blk[36] = 0b11100100               # elements 0..3: q = 0, 1, 2, 3
+    out = orc.dequantize(Q2_K, bytes(blk), 256)
+    assert list(out[:4]) == [-5.0, -2.0, 1.0, 4.0]
+    # sub-block 4 starts past the 32 code bytes: q = 1 (quant.rs:645-649)
+    assert np.all(out[64:80] == -1.0)
+
+
+def test_q3_k_hand_block(orc):
+    blk = bytearray(162)
+    blk[0:2] = bytes(_f16(2.0))
+    blk[2] = 0x75                      # elements 0, 1: 3-bit fields 5 and 7
+    blk[66] = 0b00000100               # element 1 (bit 2) gets bit 3 set
+    blk[130] = 3                       # scale of elements 0..7
+    out = orc.dequantize(Q3_K, bytes(blk), 256)
+    assert out[0] == (5 - 16) * 2 * 3 and out[1] == ((7 | 8) - 16) * 2 * 3
+    assert out[2] == -16 * 2 * 3
+
+
+def test_q8_k_hand_block(orc):
+    blk = bytearray(258)
+    blk[0:2] = bytes(_f16(0.5))
+    blk[2], blk[3], blk[257] = 0x80, 0x7F, 0x01
+    out = orc.dequantize(Q8_K, bytes(blk), 256)
+    assert out[0] == -64.0 and out[1] == 63.5 and out[255] == 0.5
+
+
+def test_k_quant_signed_zeros(orc):
+    """All-zero blocks: the reference's operation order leaves -0.0 where no addition
+    follows (Q3_K, Q6_K: (q < 0) * 0 * 0) and +0.0 where one does (Q2_K, Q4_K, Q5_K)."""
+    for qt, neg in ((Q3_K, True), (Q6_K, True), (Q2_K, False), (Q4_K, False), (Q5_K, False)):
+        out = orc.dequantize(qt, bytes(orc.BYTES_PER_BLOCK[qt]), 256)
+        assert np.all(out == 0.0) and np.all(np.signbit(out) == neg), qt
+
+
+@pytest.mark.parametrize("qt", [Q4_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K])
+def test_short_input_stops_at_first_incomplete_block(orc, qt):
+    bpb, bs = orc.BYTES_PER_BLOCK[qt], orc.BLOCK_SIZE[qt]
+    rng = np.random.default_rng(qt)
+    data = rng.integers(0, 256, 3 * bpb, dtype=np.uint8)
+    data[1::max(bpb // 2, 1)] &= 0x3B  # keep fp16 scales finite-ish
+    full = orc.dequantize(qt, data, 3 * bs)
+    part = orc.dequantize(qt, data[: 2 * bpb + bpb // 2], 3 * bs)
+    assert np.array_equal(part[: 2 * bs].view(np.uint32), full[: 2 * bs].view(np.uint32))
+    assert np.all(part[2 * bs:] == 0.0)
+
+
+def test_safe_dequantize_q4_1_regression_generator(orc):
+    # tests/quant_simd_regression_test.rs:257-275: sizes 32..256 are Ok and finite
+    for n in (32, 64, 128, 256):
+        st, out, _ = orc.safe_dequantize(Q4_1, orc.create_test_q4_1_data(n), n)
+        assert st == 0 and out.size == n and np.all(np.isfinite(out))
+    # block 1 of the generator: d = f16(0.165), m = f16(-0.9), byte j = (16 + j) % 16 twice
+    data = orc.create_test_q4_1_data(64)
+    d = np.float32(np.float16(np.float32(0.15) + np.float32(0.015)))
+    m = np.float32(np.float16(np.float32(-1.0) + np.float32(0.1)))
+    out = orc.dequantize(Q4_1, data, 64)
+    assert out[32 + 2 * 5] == np.float32(np.float32(5) * d) + m
