@@ -50,7 +50,8 @@ typedef enum {
     OPENMINI_QMM_ERR_INFERENCE = -4,     /* = OPENMINI_ERR_INFERENCE */
     OPENMINI_QMM_ERR_UNSUPPORTED = -5,   /* = OPENMINI_ERR_UNSUPPORTED: QuantError::UnsupportedType */
     OPENMINI_QMM_ERR_HIP = -10,          /* HIP runtime failure (no device, launch error, ...) */
-    OPENMINI_QMM_ERR_INSUFFICIENT_DATA = -11 /* QuantError::InsufficientData{expected, actual} */
+    OPENMINI_QMM_ERR_INSUFFICIENT_DATA = -11, /* QuantError::InsufficientData{expected, actual} */
+    OPENMINI_QMM_ERR_NOT_FOUND = -12     /* "Tensor not found" / missing metadata key */
 } openmini_qmm_status_t;
 
 /* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload, GEMV and
@@ -186,6 +187,87 @@ int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf
 
 /* Same on host memory, synchronous. */
 int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out);
+
+/* ---- GGUF files: the loader's raw-block path ----------------------------------------
+ * GgufFile (src/model/inference/gguf.rs:1357-2110) and QuantizedWeightLoader
+ * (quant_loader.rs:54-138) without dequantize-at-load.  The file is memory-mapped once;
+ * tensor bytes are views of the mapping; a Q4_0 / Q8_0 projection goes to the GPU as
+ * its raw blocks.  Host-only calls (open, header, lookups, metadata, data views) touch
+ * no device. */
+
+typedef struct openmini_qmm_gguf openmini_qmm_gguf_t;
+
+typedef enum {
+    OPENMINI_QMM_GGUF_AUTO = 0,      /* standard, else the reference's dialect */
+    OPENMINI_QMM_GGUF_REFERENCE = 1, /* 1-byte type fields, absolute tensor offsets (gguf.rs:1795,
+                                        2009, 2037) -- what the reference reads and writes */
+    OPENMINI_QMM_GGUF_STANDARD = 2   /* GGUF v2/v3: uint32 type fields, offsets relative to the
+                                        data section aligned to general.alignment (default 32) */
+} openmini_qmm_gguf_dialect_t;
+
+typedef struct {
+    uint32_t version;            /* GgufHeader (gguf.rs:1687-1702) */
+    int32_t dialect;             /* the dialect the file was read in */
+    uint64_t tensor_count;
+    uint64_t metadata_kv_count;
+    uint64_t distinct_tensors;   /* after later definitions replace earlier ones */
+    uint64_t distinct_keys;
+    uint32_t alignment;          /* standard dialect; 0 for the reference's */
+    uint64_t file_size;
+} openmini_qmm_gguf_header_t;
+
+typedef struct {
+    int32_t type;                /* GgufTensorType id (gguf.rs:219-247) */
+    uint32_t n_dims;
+    uint64_t dims[8];            /* GGUF order: dims[0] = ne0 (the contiguous dimension) */
+    uint64_t offset;             /* absolute file offset of the data */
+    uint64_t n_elements;         /* GgufTensor::num_elements (gguf.rs:425-427) */
+    uint64_t data_size;          /* GgufTensor::data_size (gguf.rs:431-438) */
+} openmini_qmm_gguf_tensor_info_t;
+
+/* GgufFile::open + parse (gguf.rs:1357-1364, 1658-2032).  Errors (MODEL_LOAD, message as
+ * the reference's): file missing, "File too small", "Invalid GGUF magic number",
+ * "Unexpected EOF", "String too long", "Unknown value type", "Too many dimensions",
+ * "Unknown tensor type".  Never reads past the file. */
+int openmini_qmm_gguf_open(const char* path, int dialect, openmini_qmm_gguf_t** out_gguf);
+void openmini_qmm_gguf_close(openmini_qmm_gguf_t* gguf);
+int openmini_qmm_gguf_header(const openmini_qmm_gguf_t* gguf, openmini_qmm_gguf_header_t* header);
+
+/* Tensors in file order (index < distinct_tensors) and by name (GgufFile::tensors). */
+int openmini_qmm_gguf_tensor_name(const openmini_qmm_gguf_t* gguf, size_t index, char* buf, size_t buf_len);
+int openmini_qmm_gguf_tensor_info(const openmini_qmm_gguf_t* gguf, const char* name,
+                                  openmini_qmm_gguf_tensor_info_t* info);
+
+/* GgufFile::get_tensor_data (gguf.rs:2034-2045): a view of the tensor's data_size bytes
+ * inside the mapping, valid until openmini_qmm_gguf_close.  NOT_FOUND; MODEL_LOAD
+ * "Tensor data out of bounds". */
+int openmini_qmm_gguf_tensor_data(const openmini_qmm_gguf_t* gguf, const char* name, const void** data,
+                                  size_t* bytes);
+
+/* GgufMetadata (gguf.rs:133-209): keys in file order, value type (0..12, gguf.rs:73-101)
+ * and the typed getters get_u32 (UInt32 | Int32), get_u64 (UInt64 | Int64 | UInt32 |
+ * Int32), get_f32 (Float32), get_string.  NOT_FOUND when absent or of another type. */
+int openmini_qmm_gguf_meta_key(const openmini_qmm_gguf_t* gguf, size_t index, char* buf, size_t buf_len);
+int openmini_qmm_gguf_meta_type(const openmini_qmm_gguf_t* gguf, const char* key, int* value_type,
+                                uint64_t* array_len);
+int openmini_qmm_gguf_get_u32(const openmini_qmm_gguf_t* gguf, const char* key, uint32_t* out);
+int openmini_qmm_gguf_get_u64(const openmini_qmm_gguf_t* gguf, const char* key, uint64_t* out);
+int openmini_qmm_gguf_get_f32(const openmini_qmm_gguf_t* gguf, const char* key, float* out);
+int openmini_qmm_gguf_get_string(const openmini_qmm_gguf_t* gguf, const char* key, char* buf, size_t buf_len,
+                                 size_t* out_len);
+
+/* QuantizedWeightLoader::load_tensor (quant_loader.rs:66-92) without dequantization: the
+ * 2-D tensor [ne0 = K, ne1 = N] becomes the weight W[N, K] (row n = K consecutive
+ * elements, the semantic layout linear() multiplies by); Q4_0 / Q8_0 only (UNSUPPORTED
+ * otherwise).  Copy and repack run on `stream`, synchronised before returning. */
+int openmini_qmm_gguf_upload_weight(const openmini_qmm_gguf_t* gguf, const char* name, void* stream,
+                                    openmini_qweight_t** out_weight);
+
+/* GgufFile::get_tensor_data_by_ref (gguf.rs:2062-2110) on the GPU: the tensor as
+ * n_elements f32 in device memory at d_out, bit-identical to the reference for F32, F16,
+ * Q4_0, Q4_1, Q8_0 and Q2_K..Q8_K (UNSUPPORTED for other types).  Synchronous. */
+int openmini_qmm_gguf_dequantize_tensor(const openmini_qmm_gguf_t* gguf, const char* name, float* d_out,
+                                        void* stream);
 
 /* ---- device memory and streams for callers without a HIP binding of their own ----- */
 

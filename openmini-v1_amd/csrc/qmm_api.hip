@@ -161,6 +161,64 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 }  // namespace
 
+namespace qmm {
+
+void set_last_error(const char* msg) { g_last_error = msg ? msg : ""; }
+
+int upload_from_host(int type, const void* host_blocks, size_t bytes, int64_t n_rows, int64_t k_cols, void* stream,
+                     openmini_qweight** out_weight) {
+    *out_weight = nullptr;
+    int rc = validate_weight_args(type, bytes, n_rows, k_cols);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!host_blocks) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null gguf_blocks");
+    int dev = 0;
+    rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t need = (size_t)n_rows * (size_t)(k_cols / kQK) * bytes_per_block(type);
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, need);
+    if (e != hipSuccess)
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) staging failed: %s", need, hipGetErrorString(e));
+    openmini_qweight* h = nullptr;
+    rc = alloc_weight(type, n_rows, k_cols, dev, &h);
+    if (rc != OPENMINI_QMM_OK) {
+        (void)hipFree(staging);
+        return rc;
+    }
+    hipStream_t s = as_stream(stream);
+    e = hipMemcpyAsync(staging, host_blocks, need, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = clear_padding(h->w, s);
+    if (e == hipSuccess) e = launch_repack(h->w, static_cast<const uint8_t*>(staging), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(staging);
+    if (e != hipSuccess) {
+        openmini_qmm_free_weight(h);
+        return hip_fail(e, "upload/repack");
+    }
+    *out_weight = h;
+    return ok();
+}
+
+int dequantize_from_host(int type, const void* host, size_t bytes, size_t n, float* d_out, void* stream) {
+    if (n == 0) return ok();
+    int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t used = bytes;
+    void* din = nullptr;
+    hipError_t e = hipMalloc(&din, used ? used : 1);
+    if (e != hipSuccess)
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) for dequantize failed: %s", used, hipGetErrorString(e));
+    hipStream_t s = as_stream(stream);
+    if (used) e = hipMemcpyAsync(din, host, used, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = launch_dequant_layout(type, static_cast<const uint8_t*>(din), used, n, d_out, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(din);
+    if (e != hipSuccess) return hip_fail(e, "dequantize");
+    return ok();
+}
+
+}  // namespace qmm
+
 extern "C" {
 
 const char* openmini_qmm_version(void) { return OPENMINI_QMM_VERSION_STRING; }
@@ -218,35 +276,7 @@ size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements) {
 int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes, int64_t n_rows,
                         int64_t k_cols, openmini_qweight_t** out_weight) {
     if (!out_weight) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_weight");
-    *out_weight = nullptr;
-    int rc = validate_weight_args(type, gguf_bytes, n_rows, k_cols);
-    if (rc != OPENMINI_QMM_OK) return rc;
-    if (!gguf_blocks) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null gguf_blocks");
-    int dev = 0;
-    rc = ensure_device(&dev);
-    if (rc != OPENMINI_QMM_OK) return rc;
-    const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
-    void* staging = nullptr;
-    hipError_t e = hipMalloc(&staging, need);
-    if (e != hipSuccess)
-        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) staging failed: %s", need, hipGetErrorString(e));
-    openmini_qweight* h = nullptr;
-    rc = alloc_weight(type, n_rows, k_cols, dev, &h);
-    if (rc != OPENMINI_QMM_OK) {
-        (void)hipFree(staging);
-        return rc;
-    }
-    e = hipMemcpy(staging, gguf_blocks, need, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = clear_padding(h->w, nullptr);
-    if (e == hipSuccess) e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(staging), nullptr);
-    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
-    (void)hipFree(staging);
-    if (e != hipSuccess) {
-        openmini_qmm_free_weight(h);
-        return hip_fail(e, "upload/repack");
-    }
-    *out_weight = h;
-    return ok();
+    return qmm::upload_from_host(type, gguf_blocks, gguf_bytes, n_rows, k_cols, nullptr, out_weight);
 }
 
 int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_bytes, int64_t n_rows,

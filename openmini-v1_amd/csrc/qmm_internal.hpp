@@ -34,6 +34,8 @@
 
 #include "../../include/openmini_qmm.h"
 
+struct openmini_qweight;
+
 namespace qmm {
 
 constexpr int kQK = 32;
@@ -136,5 +138,19 @@ hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, si
                                  hipStream_t s);
 
 hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+// ---- shared host helpers (qmm_api.hip) ----------------------------------------------
+
+// Sets the calling thread's openmini_qmm_last_error() message.
+void set_last_error(const char* msg);
+
+// Host GGUF blocks of W[n_rows, k_cols] -> a new repacked weight handle (validated like
+// openmini_qmm_upload); the copy and repack run on `stream`, which is synchronised.
+int upload_from_host(int type, const void* host_blocks, size_t bytes, int64_t n_rows, int64_t k_cols, void* stream,
+                     openmini_qweight** out_weight);
+
+// Host bytes of any layout of launch_dequant_layout -> n floats at d_out (device),
+// quant::dequantize semantics; synchronous on `stream`.
+int dequantize_from_host(int type, const void* host, size_t bytes, size_t n, float* d_out, void* stream);
 
 }  // namespace qmm

@@ -19,6 +19,7 @@ ERR_INFERENCE = -4
 ERR_UNSUPPORTED = -5
 ERR_HIP = -10
 ERR_INSUFFICIENT_DATA = -11
+ERR_NOT_FOUND = -12
 
 Q4_0 = 2
 Q8_0 = 7
@@ -33,6 +34,30 @@ class WeightInfo(ctypes.Structure):
         ("blocks_per_row", ctypes.c_int64),
         ("gguf_bytes", ctypes.c_size_t),
         ("device_bytes", ctypes.c_size_t),
+    ]
+
+
+class GgufHeader(ctypes.Structure):
+    _fields_ = [
+        ("version", ctypes.c_uint32),
+        ("dialect", ctypes.c_int32),
+        ("tensor_count", ctypes.c_uint64),
+        ("metadata_kv_count", ctypes.c_uint64),
+        ("distinct_tensors", ctypes.c_uint64),
+        ("distinct_keys", ctypes.c_uint64),
+        ("alignment", ctypes.c_uint32),
+        ("file_size", ctypes.c_uint64),
+    ]
+
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_int32),
+        ("n_dims", ctypes.c_uint32),
+        ("dims", ctypes.c_uint64 * 8),
+        ("offset", ctypes.c_uint64),
+        ("n_elements", ctypes.c_uint64),
+        ("data_size", ctypes.c_uint64),
     ]
 
 
@@ -62,6 +87,20 @@ SIGNATURES = {
     "openmini_qmm_dequantize": (_i, [_i, _p, _sz, _sz, _p, ctypes.POINTER(_sz)]),
     "openmini_qmm_dequantize_any_device": (_i, [_i, _p, _sz, _sz, _p, _p]),
     "openmini_qmm_dequantize_any": (_i, [_i, _p, _sz, _sz, _p]),
+    "openmini_qmm_gguf_open": (_i, [ctypes.c_char_p, _i, ctypes.POINTER(_p)]),
+    "openmini_qmm_gguf_close": (None, [_p]),
+    "openmini_qmm_gguf_header": (_i, [_p, ctypes.POINTER(GgufHeader)]),
+    "openmini_qmm_gguf_tensor_name": (_i, [_p, _sz, ctypes.c_char_p, _sz]),
+    "openmini_qmm_gguf_tensor_info": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(GgufTensorInfo)]),
+    "openmini_qmm_gguf_tensor_data": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(_p), ctypes.POINTER(_sz)]),
+    "openmini_qmm_gguf_meta_key": (_i, [_p, _sz, ctypes.c_char_p, _sz]),
+    "openmini_qmm_gguf_meta_type": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_uint64)]),
+    "openmini_qmm_gguf_get_u32": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)]),
+    "openmini_qmm_gguf_get_u64": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "openmini_qmm_gguf_get_f32": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+    "openmini_qmm_gguf_get_string": (_i, [_p, ctypes.c_char_p, ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]),
+    "openmini_qmm_gguf_upload_weight": (_i, [_p, ctypes.c_char_p, _p, ctypes.POINTER(_p)]),
+    "openmini_qmm_gguf_dequantize_tensor": (_i, [_p, ctypes.c_char_p, _p, _p]),
     "openmini_qmm_malloc": (_i, [ctypes.POINTER(_p), _sz]),
     "openmini_qmm_free": (_i, [_p]),
     "openmini_qmm_memcpy_h2d": (_i, [_p, _p, _sz, _p]),
