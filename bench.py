@@ -227,6 +227,57 @@ def cpu_baseline(gemv: dict, seconds: float) -> dict:
     }
 
 
+def bench_layer(qmm, hipr, stream, steps, warmup, qtype=Q4_0, H=4096, I=11008, seed=0x5EED0010):
+    """One Llama-7B decode layer's seven projections at batch 1 (q, k, v, o [H, H];
+    gate, up [I, H]; down [H, I]) over distinct layers' weights (>= 1 GiB rotated):
+    grouped as 4 launches (q/k/v together, o, gate/up with the silu * up epilogue,
+    down) and, for comparison, as 7 single-weight launches plus nothing else (the
+    grouped path also does the SwiGLU product the separate path leaves out)."""
+    from openmini_qmm import synth
+    shapes = [(H, H)] * 4 + [(I, H), (I, H), (H, I)]
+    blocks = [synth.weight_blocks(qtype, n, k, seed=seed + i) for i, (n, k) in enumerate(shapes)]
+    layer_bytes = sum(b.size for b in blocks)
+    copies = max(2, -(-MALL_DEFEAT_BYTES // layer_bytes))
+    log(f"layer type={qtype}: {copies} layers x {layer_bytes} B")
+    layers = [[qmm.QuantizedWeight(qtype, b, n, k) for b, (n, k) in zip(blocks, shapes)]
+              for _ in range(copies)]
+    x = synth.normal(seed + 0x8000, (1, H), 1.0)
+    dx = qmm.DeviceBuffer.from_numpy(x)
+    dq, dk, dv, do, dd = (qmm.DeviceBuffer(H * 4) for _ in range(5))
+    dg, du, dh = (qmm.DeviceBuffer(I * 4) for _ in range(3))
+    sh = stream.handle
+
+    def grouped(i):
+        q, k, v, o, g, u, d = layers[i % copies]
+        qmm.gemv_multi((q, k, v), dx, (dq, dk, dv), 1, sh)
+        o.gemv(dx, do, 1, sh)
+        qmm.ffn_gate_up(g, u, dx, dh, 1, sh)
+        d.gemv(dh, dd, 1, sh)
+
+    def separate(i):
+        q, k, v, o, g, u, d = layers[i % copies]
+        q.gemv(dx, dq, 1, sh)
+        k.gemv(dx, dk, 1, sh)
+        v.gemv(dx, dv, 1, sh)
+        o.gemv(dx, do, 1, sh)
+        g.gemv(dx, dg, 1, sh)
+        u.gemv(dx, du, 1, sh)
+        d.gemv(dh, dd, 1, sh)
+
+    res = {"H": H, "I": I, "layer_bytes": layer_bytes, "layers": copies}
+    for name, fn in (("grouped", grouped), ("separate", separate)):
+        for i in range(warmup):
+            fn(i)
+        stream.synchronize()
+        ms = time_steps(fn, steps, sh, hipr)
+        res[name + "_us"] = ms / steps * 1e3
+        res[name + "_gbs"] = layer_bytes * steps / (ms * 1e-3) / 1e9
+    for ws in layers:
+        for w in ws:
+            w.close()
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,6 +286,7 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
+    ap.add_argument("--no-layer", action="store_true", help="skip the decode-layer leg")
     ap.add_argument("--eager", action="store_true",
                     help="launch directly instead of replaying a HIP graph (for counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -264,6 +316,11 @@ def main(argv=None) -> int:
         gemm = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
         log(f"q8_0 gemm M=512: wall {gemm['tflops_wall']:.1f} TFLOP/s, kernel "
             f"{gemm['tflops_kernel']:.1f} TFLOP/s")
+    layer = None
+    if not args.no_layer:
+        layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
+        log(f"decode layer: grouped {layer['grouped_us']:.2f} us ({layer['grouped_gbs']:.1f} GB/s), "
+            f"separate {layer['separate_us']:.2f} us ({layer['separate_gbs']:.1f} GB/s)")
     copy = None
     if args.calibrate_copy:
         copy = copy_calibration(qmm, hipr, stream)
@@ -311,6 +368,14 @@ def main(argv=None) -> int:
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
                          "kernel_us": round(gemm["kernel_ms"] * 1e3, 3)},
+        }
+    if layer:
+        out["decode_layer"] = {
+            "workload": "q4_0_llama7b_layer_7proj_b1", "unit": "GB/s",
+            "value": round(layer["grouped_gbs"], 2), "us_per_layer": round(layer["grouped_us"], 3),
+            "launches": 4, "separate_gbs": round(layer["separate_gbs"], 2),
+            "separate_us_per_layer": round(layer["separate_us"], 3), "separate_launches": 7,
+            "layer_bytes": layer["layer_bytes"], "layers_rotated": layer["layers"],
         }
     print(json.dumps(out), flush=True)
     return 0

@@ -151,6 +151,27 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
 int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
                            int64_t m, void* stream);
 
+/* ---- projections of one layer (src/model/inference/model.rs) ----------------------- */
+
+/* Weights that share the input in one launch per 4 batch rows: d_ys[i][batch, N_i] =
+ * x[batch, K] . W_i^T for i < count (1..4), all of one type and one K.  Replaces the
+ * three linear_gemm calls of prepare_qkv (model.rs:1392-1394: q, k, v of one
+ * normalised hidden state).  d_x must be 16-byte aligned. */
+int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count, const float* d_x,
+                            float* const* d_ys, int64_t batch, void* stream);
+
+/* FFN hidden state of FFNWeights::forward (model.rs:728-731, the silu(gate) * up
+ * branch; silu(v) = v / (1 + exp(-v)), model.rs:1187-1189):
+ * d_h[batch, N] = silu(x . Wg^T) * (x . Wu^T), gate and up of one type and shape, one
+ * launch per 4 batch rows reading both weights.  d_x must be 16-byte aligned. */
+int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qweight_t* up,
+                             const float* d_x, float* d_h, int64_t batch, void* stream);
+
+/* The same for prefill with bf16 activations (raw bf16 bits): the gate GEMM writes
+ * d_h, the up GEMM finishes silu(gate) * up in its epilogue.  d_x 16-byte aligned. */
+int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini_qweight_t* up,
+                                  const uint16_t* d_x, float* d_h, int64_t m, void* stream);
+
 /* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
  * fp32 in/out, synchronous.  Uses the GEMV kernels (exact fp32 activations). */
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,

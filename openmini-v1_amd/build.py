@@ -31,6 +31,9 @@ COMMON = [
     # MFMA results in VGPRs: the kernels post-process every MFMA result on the VALU,
     # and the AGPR form costs a v_accvgpr_read per element and serialises the MFMAs.
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # The first kernel arguments arrive in SGPRs (gfx950 kernarg preloading): a
+    # launch-bound kernel starts without waiting on a scalar load of its arguments.
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-I", os.path.join(ROOT, "include"),
 ]
 

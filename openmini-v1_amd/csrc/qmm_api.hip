@@ -356,6 +356,80 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     return ok();
 }
 
+int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count, const float* d_x,
+                            float* const* d_ys, int64_t batch, void* stream) {
+    if (!weights || !d_ys) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null weights or outputs");
+    if (count < 1 || count > qmm::kMaxGroup)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "count=%d must be in [1, %d]", count, qmm::kMaxGroup);
+    const qmm::Weight* ws[qmm::kMaxGroup];
+    for (int i = 0; i < count; ++i) {
+        int rc = check_weight(weights[i]);
+        if (rc != OPENMINI_QMM_OK) return rc;
+        if (!d_ys[i]) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null output %d", i);
+        ws[i] = &weights[i]->w;
+        if (ws[i]->type != ws[0]->type || ws[i]->k != ws[0]->k || ws[i]->device != ws[0]->device)
+            return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "weight %d differs from weight 0 in type, K or device", i);
+    }
+    if (!d_x) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x");
+    if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    int64_t tiles = 0;
+    for (int i = 0; i < count; ++i) tiles += ws[i]->n_tiles;
+    if (tiles > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "too many rows in one group");
+    const int64_t k = ws[0]->k;
+    for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
+        const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
+        float* ys[qmm::kMaxGroup];
+        for (int i = 0; i < count; ++i) ys[i] = d_ys[i] + b0 * ws[i]->n;
+        hipError_t e = qmm::launch_gemv_group(ws, ys, count, d_x + b0 * k, nb, false, as_stream(stream));
+        if (e != hipSuccess) return hip_fail(e, "gemv_multi launch");
+    }
+    return ok();
+}
+
+static int check_pair(const openmini_qweight_t* gate, const openmini_qweight_t* up) {
+    int rc = check_weight(gate);
+    if (rc == OPENMINI_QMM_OK) rc = check_weight(up);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const qmm::Weight &g = gate->w, &u = up->w;
+    if (g.type != u.type || g.n != u.n || g.k != u.k || g.device != u.device)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM,
+                    "gate [%lld, %lld] and up [%lld, %lld] differ in shape, type or device", (long long)g.n,
+                    (long long)g.k, (long long)u.n, (long long)u.k);
+    return OPENMINI_QMM_OK;
+}
+
+int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qweight_t* up, const float* d_x,
+                             float* d_h, int64_t batch, void* stream) {
+    int rc = check_pair(gate, up);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
+    if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    const qmm::Weight* ws[2] = {&gate->w, &up->w};
+    const int64_t n = gate->w.n, k = gate->w.k;
+    for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
+        const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
+        float* ys[2] = {d_h + b0 * n, d_h + b0 * n};
+        hipError_t e = qmm::launch_gemv_group(ws, ys, 2, d_x + b0 * k, nb, true, as_stream(stream));
+        if (e != hipSuccess) return hip_fail(e, "ffn_gate_up launch");
+    }
+    return ok();
+}
+
+int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini_qweight_t* up,
+                                  const uint16_t* d_x, float* d_h, int64_t m, void* stream) {
+    int rc = check_pair(gate, up);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
+    if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    hipError_t e = qmm::launch_gemm_bf16(gate->w, d_x, d_h, m, as_stream(stream), false);
+    if (e == hipSuccess) e = qmm::launch_gemm_bf16(up->w, d_x, d_h, m, as_stream(stream), true);
+    if (e != hipSuccess) return hip_fail(e, "ffn_gate_up_bf16 launch");
+    return ok();
+}
+
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y, int64_t m) {
     int rc = check_weight(weight);
     if (rc != OPENMINI_QMM_OK) return rc;

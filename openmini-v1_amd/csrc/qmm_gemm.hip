@@ -103,7 +103,9 @@ struct Shape {
     static_assert(kTileBlocks % kSB == 0, "a step covers whole blocks of one group");
 };
 
-template <bool kQ4, int kNW, int kKS, int kSB>
+// kGate: y holds the gate projection on entry and each element is replaced by
+// silu(gate) * (x . W^T), silu(v) = v / (1 + exp(-v)) (model.rs:713-735, :1187-1189).
+template <bool kQ4, int kNW, int kKS, int kSB, bool kGate>
 __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ chunks, float* __restrict__ y,
     int m_rows, int n_rows, int n_tiles, int groups, int k) {
@@ -307,17 +309,23 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
                     for (int h = 1; h < kKS; ++h)
                         v += red[(((size_t)(h - 1) * kNW + wn) * kAcc + (i * kWT + j) * 4 + r) * 64 + lane];
                     const int gm = m0 + i * 16 + kq * 4 + r;
-                    if (full_m || gm < m_rows) yc[(size_t)gm * n_rows] = v;
+                    if (full_m || gm < m_rows) {
+                        if constexpr (kGate) {
+                            const float g = yc[(size_t)gm * n_rows];
+                            v = g / (1.0f + expf(-g)) * v;
+                        }
+                        yc[(size_t)gm * n_rows] = v;
+                    }
                 }
         }
     }
 }
 
-template <bool kQ4, int kNW, int kKS, int kSB>
+template <bool kQ4, int kNW, int kKS, int kSB, bool kGate>
 hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
     using S = Shape<kNW, kKS, kSB>;
     const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL((gemm_kernel<kQ4, kNW, kKS, kSB>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
+    hipLaunchKernelGGL((gemm_kernel<kQ4, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
                        (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     return hipGetLastError();
 }
@@ -327,16 +335,16 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m,
 // 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers overlap the other's
 // work).  Measured on MI355X against 4 x 2 (128 x 192) with 2- and 4-block K steps:
 // equal or faster on Q8_0 11008 x 4096 at M = 128 / 512 / 2048.
-template <bool kQ4>
+template <bool kQ4, bool kGate>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
-    if (m <= kBM) return launch_shape<kQ4, 1, 4, 2>(w, x, y, m, s);
-    return launch_shape<kQ4, 2, 2, 2>(w, x, y, m, s);
+    if (m <= kBM) return launch_shape<kQ4, 1, 4, 2, kGate>(w, x, y, m, s);
+    return launch_shape<kQ4, 2, 2, 2, kGate>(w, x, y, m, s);
 }
 
 }  // namespace
 
-hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m,
-                            hipStream_t s) {
+hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
+                            bool gate_in_y) {
     // x offsets are 32-bit: launches cover row ranges whose x is below 2 GiB.
     const int64_t rows_per_launch = ((((int64_t)1 << 31) - 1) / (w.k * 2)) / kBM * kBM;
     if (rows_per_launch <= 0) return hipErrorInvalidValue;  // one row tile of x exceeds 2 GiB
@@ -344,8 +352,11 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
         const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
         const uint16_t* xs = x + m_off * w.k;
         float* ys = y + m_off * w.n;
-        const hipError_t e = w.type == OPENMINI_QMM_Q4_0 ? launch_kind<true>(w, xs, ys, mm, s)
-                                                         : launch_kind<false>(w, xs, ys, mm, s);
+        const bool q4 = w.type == OPENMINI_QMM_Q4_0;
+        const hipError_t e = gate_in_y ? (q4 ? launch_kind<true, true>(w, xs, ys, mm, s)
+                                             : launch_kind<false, true>(w, xs, ys, mm, s))
+                                       : (q4 ? launch_kind<true, false>(w, xs, ys, mm, s)
+                                             : launch_kind<false, false>(w, xs, ys, mm, s));
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

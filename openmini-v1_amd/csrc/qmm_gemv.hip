@@ -31,6 +31,14 @@
 // product for row n, in lane (n, t), register h.  Two MFMAs cover a block's 32
 // elements.
 //
+// One launch can serve several weights that share x and K:
+//   * kGroup: up to kMaxGroup weights (q / k / v projections); workgroup i takes
+//     tile i - tile_begin[g] of weight g, where tile_begin partitions the grid;
+//   * kPair: one (gate, up) pair of equal shape; every workgroup runs the same tile
+//     of both weights on the same activation digits and writes silu(gate) * up, the
+//     hidden state of the FFN (model.rs:713-735 with silu at :1187-1189:
+//     v / (1 + exp(-v))).
+//
 // Work split: a workgroup owns one 16-row tile; its W waves split the K groups into
 // contiguous slices (contiguous runs of the weight).  A wave walks its slice in
 // phases of up to P groups: it first issues the phase's activation loads (L2 hits,
@@ -74,34 +82,76 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// The weights of one launch (kernel argument, uniform).
+struct GemvGroup {
+    int tile_begin[kMaxGroup + 1];     // grid partition: weight g owns [tile_begin[g], tile_begin[g+1]);
+                                       // entries past the last weight hold the grid size
+    const uint8_t* chunks[kMaxGroup];  // a pair: [0] gate, [1] up
+    float* y[kMaxGroup];
+    int n_rows[kMaxGroup];
+};
+
 // LDS A-fragment slots of one wave for one phase: [p][b][u = block half][t = block
 // slot][h = digit], 16 bytes each, then one zero slot read by lanes whose A fragment
 // is zero.
 template <int B, int P>
 constexpr int kSlots = P * B * 2 * 4 * 3 + 1;
 
-template <bool kQ4, int B, int W, int P>
-__global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict__ chunks,
-                                                      const float* __restrict__ x,
-                                                      float* __restrict__ y, int n_rows, int n_tiles,
-                                                      int groups, int k) {
+// The leading arguments describe weight 0 (and the up weight of a pair) and fit the
+// SGPRs the kernel arguments are preloaded into; `grp` is read only by workgroups of
+// the later weights of a group.
+// Launch kinds: one weight, a group of weights sharing x (tiles partitioned), or a
+// (gate, up) pair run on the same tiles.
+constexpr int kOne = 0, kGroup = 1, kPair = 2;
+
+template <bool kQ4, int B, int W, int P, int kKind>
+__global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict__ w0,
+                                                      const uint8_t* __restrict__ w1,
+                                                      const float* __restrict__ x, float* __restrict__ y0,
+                                                      int n_rows0, int tiles0, int groups, int k,
+                                                      const GemvGroup grp) {
+    constexpr int kNW = kKind == kPair ? 2 : 1;  // weights per tile
     constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kCodeBytes = kTileEntries * kCB;
     constexpr int kChunk = chunk_bytes_for(kQ4);
     constexpr int kS = kSlots<B, P>;
     constexpr int kZero = kS - 1;
     __shared__ uint4 a_lds[W][kS];
-    __shared__ float red[W][B][16];
+    __shared__ float red[W][kNW][B][16];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wave
     const int ln = lane & 15, lt = lane >> 4;
-    const int tile = blockIdx.x;
+    // This workgroup's weight (uniform): weight 0 below tiles0, else the last g with
+    // tile_begin[g] <= blockIdx.x (entries past the group's count hold the grid size).
+    int tile_lo = 0, tile_hi = tiles0, n_rows = n_rows0;
+    float* __restrict__ y = y0;
+    const uint8_t* wp[kNW];
+    wp[0] = w0;
+    if constexpr (kNW == 2) wp[1] = w1;
+    if constexpr (kKind == kGroup) {
+        if ((int)blockIdx.x >= tiles0) {
+#pragma unroll
+            for (int i = 1; i < kMaxGroup; ++i) {
+                const bool mine = (int)blockIdx.x >= grp.tile_begin[i];
+                tile_lo = mine ? grp.tile_begin[i] : tile_lo;
+                tile_hi = mine ? grp.tile_begin[i + 1] : tile_hi;
+                n_rows = mine ? grp.n_rows[i] : n_rows;
+                y = mine ? grp.y[i] : y;
+                wp[0] = mine ? grp.chunks[i] : wp[0];
+            }
+        }
+    }
+    const int tile = (int)blockIdx.x - tile_lo;
+    const int n_tiles = tile_hi - tile_lo;
     const int g0 = (int)((int64_t)groups * wave / W);
     const int g1 = (int)((int64_t)groups * (wave + 1) / W);
 
     // The chunks are < 4 GiB (checked at upload), so 32-bit buffer offsets suffice.
-    const __amdgpu_buffer_rsrc_t w_rs = make_rsrc(chunks, (uint32_t)n_tiles * groups * kChunk);
+    __amdgpu_buffer_rsrc_t w_rs[kNW];
+#pragma unroll
+    for (int nw = 0; nw < kNW; ++nw)
+        w_rs[nw] = make_rsrc(wp[nw], (uint32_t)n_tiles * groups * kChunk);
     __amdgpu_buffer_rsrc_t x_rs[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) x_rs[b] = make_rsrc(x + (size_t)b * k, (uint32_t)k * 4);
@@ -117,13 +167,18 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
     // halfword ln % 8 (a slot is 8 halfwords).
     uint16_t* wr16 = reinterpret_cast<uint16_t*>(my_lds) + ((ln >> 3) * 12 + lt * 3) * 8 + (ln & 7);
 
-    float acc[B];
+    float acc[kNW][B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+    for (int nw = 0; nw < kNW; ++nw)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[nw][b] = 0.0f;
     // Max of the rounded activations' bit patterns t = 1.5 * 2^23 + X.  Finite x gives
     // t in [2^23, 2^24] (bits <= 0x4B800000); a NaN or +-inf x makes t NaN or +-inf,
-    // whose bits lie above.
-    uint32_t seen = 0;
+    // whose bits lie above.  Tracked per batch row: a non-finite row poisons only its
+    // own outputs.
+    uint32_t seen[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) seen[b] = 0;
 
     for (int g = g0; g < g1; g += P) {
         // A phase is straight-line code (branches would make the compiler wait for
@@ -133,8 +188,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int p = 0; p < P; ++p) gp[p] = min(g + p, g1 - 1);
         float2 xv[P][B];
-        uint4 c[P][kQ4 ? 1 : 2];
-        uint32_t sc[P];
+        uint4 c[kNW][P][kQ4 ? 1 : 2];
+        uint32_t sc[kNW][P];
         // activations first: L2 hits that land before the weights do
 #pragma unroll
         for (int p = 0; p < P; ++p)
@@ -145,10 +200,15 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const uint32_t soff = tile_off + (uint32_t)gp[p] * kChunk;
-            c[p][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs, lane * kCB, soff, 0));
-            if constexpr (!kQ4)
-                c[p][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs, lane * kCB + 16, soff, 0));
-            sc[p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, kCodeBytes + lane * 2, soff, 0);
+#pragma unroll
+            for (int nw = 0; nw < kNW; ++nw) {
+                c[nw][p][0] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * kCB, soff, 0));
+                if constexpr (!kQ4)
+                    c[nw][p][1] = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * kCB + 16, soff, 0));
+                sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kCodeBytes + lane * 2, soff, 0);
+            }
         }
 
         // digits of the phase's activation blocks -> LDS, while the chunks are in flight
@@ -164,7 +224,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                 // t = 1.5 * 2^23 + round(x * 2^s): bits(t) = 0x4B400000 + X (|X| <= 2^22)
                 const uint32_t t0 = __float_as_uint(__builtin_amdgcn_ldexpf(x0, shift[p][b]) + 12582912.0f);
                 const uint32_t t1 = __float_as_uint(__builtin_amdgcn_ldexpf(x1, shift[p][b]) + 12582912.0f);
-                seen = max(seen, max(t0, t1));
+                seen[b] = max(seen[b], max(t0, t1));
                 // low three bytes of (X + 0x808080) ^ 0x808080: digits c, b, a
                 const uint32_t z0 = (t0 + (0x808080u - 0x4B400000u)) ^ 0x808080u;
                 const uint32_t z1 = (t1 + (0x808080u - 0x4B400000u)) ^ 0x808080u;
@@ -178,70 +238,84 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-            i32x4 b0, b1;
-            if constexpr (kQ4) {
-                // 16 * (q - 8) as int8 bytes, elements in order
-                const uint4 w = c[p][0];
-                b0 = i32x4{(int)((w.x << 4) & 0xF0F0F0F0u), (int)(w.x & 0xF0F0F0F0u),
-                           (int)((w.y << 4) & 0xF0F0F0F0u), (int)(w.y & 0xF0F0F0F0u)};
-                b1 = i32x4{(int)((w.z << 4) & 0xF0F0F0F0u), (int)(w.z & 0xF0F0F0F0u),
-                           (int)((w.w << 4) & 0xF0F0F0F0u), (int)(w.w & 0xF0F0F0F0u)};
-            } else {
-                const uint4 w0 = c[p][0], w1 = c[p][1];
-                b0 = i32x4{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w};
-                b1 = i32x4{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-            }
-            const float d = g + p < g1 ? f16_bits_to_f32((uint16_t)sc[p]) : 0.0f;
+        for (int p = 0; p < P; ++p)
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const int base = (p * B + b) * 2 * 12;
-                const uint4 v0 = my_lds[a_live ? base + a_slot : kZero];
-                const uint4 v1 = my_lds[a_live ? base + 12 + a_slot : kZero];
-                i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                    i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w}, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                    i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w}, b1, D, 0, 0, 0);
-                // |D| <= 2^19 each: exact in fp32; the combination rounds once per step
-                const float r = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
-                acc[b] = fmaf(d, __builtin_amdgcn_ldexpf(r, -shift[p][b] - (kQ4 ? 4 : 0)), acc[b]);
+            for (int nw = 0; nw < kNW; ++nw) {
+                i32x4 b0, b1;
+                if constexpr (kQ4) {
+                    // 16 * (q - 8) as int8 bytes, elements in order
+                    const uint4 w = c[nw][p][0];
+                    b0 = i32x4{(int)((w.x << 4) & 0xF0F0F0F0u), (int)(w.x & 0xF0F0F0F0u),
+                               (int)((w.y << 4) & 0xF0F0F0F0u), (int)(w.y & 0xF0F0F0F0u)};
+                    b1 = i32x4{(int)((w.z << 4) & 0xF0F0F0F0u), (int)(w.z & 0xF0F0F0F0u),
+                               (int)((w.w << 4) & 0xF0F0F0F0u), (int)(w.w & 0xF0F0F0F0u)};
+                } else {
+                    const uint4 w0 = c[nw][p][0], w1 = c[nw][p][1];
+                    b0 = i32x4{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w};
+                    b1 = i32x4{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                }
+                const float d = g + p < g1 ? f16_bits_to_f32((uint16_t)sc[nw][p]) : 0.0f;
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    const int base = (p * B + b) * 2 * 12;
+                    const uint4 v0 = my_lds[a_live ? base + a_slot : kZero];
+                    const uint4 v1 = my_lds[a_live ? base + 12 + a_slot : kZero];
+                    i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w}, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w}, b1, D, 0, 0, 0);
+                    // |D| <= 2^19 each: exact in fp32; the combination rounds once per step
+                    const float r = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
+                    acc[nw][b] = fmaf(d, __builtin_amdgcn_ldexpf(r, -shift[p][b] - (kQ4 ? 4 : 0)), acc[nw][b]);
+                }
             }
-        }
         // The next phase rewrites this wave's slots; a wave's LDS operations complete
         // in order, so its reads above are done before those writes.
     }
 
     // Sum the four block slots (lanes n, n+16, n+32, n+48), then the W K slices.
     // Any inf / NaN activation turns the outputs into NaN.
-    const bool bad = __builtin_amdgcn_read_exec() && __ballot(seen > 0x4B800000u) != 0;
+    bool bad[B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-        float v = acc[b];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (bad) v = __builtin_nanf("");
-        if (lane < 16) red[wave][b][lane] = v;
-    }
+    for (int b = 0; b < B; ++b) bad[b] = __ballot(seen[b] > 0x4B800000u) != 0;
+#pragma unroll
+    for (int nw = 0; nw < kNW; ++nw)
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float v = acc[nw][b];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (bad[b]) v = __builtin_nanf("");
+            if (lane < 16) red[wave][nw][b][lane] = v;
+        }
     __syncthreads();
     if (wave == 0 && lane < 16) {
         const int row = tile * kTileRows + lane;
         if (row < n_rows) {
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                float v = red[0][b][lane];
+                float v[kNW];
 #pragma unroll
-                for (int w = 1; w < W; ++w) v += red[w][b][lane];
-                y[(size_t)b * n_rows + row] = v;
+                for (int nw = 0; nw < kNW; ++nw) {
+                    v[nw] = red[0][nw][b][lane];
+#pragma unroll
+                    for (int w = 1; w < W; ++w) v[nw] += red[w][nw][b][lane];
+                }
+                if constexpr (kNW == 2)
+                    y[(size_t)b * n_rows + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
+                else
+                    y[(size_t)b * n_rows + row] = v[0];
             }
         }
     }
 }
 
-template <bool kQ4, int B, int W, int P>
-hipError_t run(const Weight& w, const float* x, float* y, hipStream_t s) {
+template <bool kQ4, int B, int W, int P, int kKind>
+hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, hipStream_t s) {
     static_assert(sizeof(uint4) * W * kSlots<B, P> <= 64 * 1024, "A-fragment LDS over budget");
-    hipLaunchKernelGGL((gemv_kernel<kQ4, B, W, P>), dim3((unsigned)w.n_tiles), dim3(64 * W), 0, s,
-                       w.chunks, x, y, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+    const unsigned wgs = (unsigned)grp.tile_begin[kMaxGroup];
+    hipLaunchKernelGGL((gemv_kernel<kQ4, B, W, P, kKind>), dim3(wgs), dim3(64 * W), 0, s, grp.chunks[0],
+                       grp.chunks[1], x, grp.y[0], grp.n_rows[0], grp.tile_begin[1], (int)groups, (int)k, grp);
     return hipGetLastError();
 }
 
@@ -250,37 +324,66 @@ hipError_t run(const Weight& w, const float* x, float* y, hipStream_t s) {
 // e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  More batch rows: at most 8 (LDS and
 // registers per wave grow with the batch).  Short K: the most slices that keep 4
 // groups per wave.
-template <bool kQ4, int B>
-hipError_t run_w(const Weight& w, const float* x, float* y, hipStream_t s) {
-    const int64_t g = w.groups;
+template <bool kQ4, int B, int kKind>
+hipError_t run_w(const GemvGroup& grp, int64_t g, int64_t k, const float* x, hipStream_t s) {
     if (g >= 32) {
         if constexpr (B == 1) {
             const int64_t pad16 = (g + 63) / 64 * 64 - g, pad8 = (g + 31) / 32 * 32 - g;
-            if (pad16 <= pad8) return run<kQ4, B, 16, 4>(w, x, y, s);
+            if (pad16 <= pad8) return run<kQ4, B, 16, 4, kKind>(grp, g, k, x, s);
         }
-        return run<kQ4, B, 8, 4>(w, x, y, s);
+        return run<kQ4, B, 8, 4, kKind>(grp, g, k, x, s);
     }
-    if (g >= 16) return run<kQ4, B, 4, 4>(w, x, y, s);
-    if (g >= 8) return run<kQ4, B, 2, 4>(w, x, y, s);
-    return run<kQ4, B, 1, 4>(w, x, y, s);
+    if (g >= 16) return run<kQ4, B, 4, 4, kKind>(grp, g, k, x, s);
+    if (g >= 8) return run<kQ4, B, 2, 4, kKind>(grp, g, k, x, s);
+    return run<kQ4, B, 1, 4, kKind>(grp, g, k, x, s);
 }
 
-template <bool kQ4>
-hipError_t dispatch(const Weight& w, const float* x, float* y, int batch, hipStream_t s) {
+template <bool kQ4, int kKind>
+hipError_t dispatch(const GemvGroup& grp, int64_t g, int64_t k, const float* x, int batch, hipStream_t s) {
     switch (batch) {
-    case 1: return run_w<kQ4, 1>(w, x, y, s);
-    case 2: return run_w<kQ4, 2>(w, x, y, s);
-    case 3: return run_w<kQ4, 3>(w, x, y, s);
-    case 4: return run_w<kQ4, 4>(w, x, y, s);
+    case 1: return run_w<kQ4, 1, kKind>(grp, g, k, x, s);
+    case 2: return run_w<kQ4, 2, kKind>(grp, g, k, x, s);
+    case 3: return run_w<kQ4, 3, kKind>(grp, g, k, x, s);
+    case 4: return run_w<kQ4, 4, kKind>(grp, g, k, x, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
+hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int count, const float* x, int batch,
+                             bool swiglu, hipStream_t s) {
+    if (count < 1 || count > kMaxGroup || (swiglu && count != 2)) return hipErrorInvalidValue;
+    GemvGroup grp{};
+    const int owners = swiglu ? 1 : count;  // weights that own tiles of the grid
+    int64_t tiles = 0;
+    for (int i = 0; i < count; ++i) {
+        grp.chunks[i] = ws[i]->chunks;
+        grp.n_rows[i] = (int)ws[i]->n;
+        grp.y[i] = ys[swiglu ? 0 : i];
+        if (!swiglu || i == 0) {
+            grp.tile_begin[i] = (int)tiles;
+            tiles += ws[i]->n_tiles;
+        }
+    }
+    for (int i = owners; i <= kMaxGroup; ++i) grp.tile_begin[i] = (int)tiles;
+    if (tiles > INT32_MAX) return hipErrorInvalidValue;
+    const Weight& w0 = *ws[0];
+    const bool q4 = w0.type == OPENMINI_QMM_Q4_0;
+    if (swiglu)
+        return q4 ? dispatch<true, kPair>(grp, w0.groups, w0.k, x, batch, s)
+                  : dispatch<false, kPair>(grp, w0.groups, w0.k, x, batch, s);
+    if (count > 1)
+        return q4 ? dispatch<true, kGroup>(grp, w0.groups, w0.k, x, batch, s)
+                  : dispatch<false, kGroup>(grp, w0.groups, w0.k, x, batch, s);
+    return q4 ? dispatch<true, kOne>(grp, w0.groups, w0.k, x, batch, s)
+              : dispatch<false, kOne>(grp, w0.groups, w0.k, x, batch, s);
+}
+
 hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hipStream_t s) {
-    if (w.type == OPENMINI_QMM_Q4_0) return dispatch<true>(w, x, y, batch, s);
-    return dispatch<false>(w, x, y, batch, s);
+    const Weight* ws[1] = {&w};
+    float* ys[1] = {y};
+    return launch_gemv_group(ws, ys, 1, x, batch, false, s);
 }
 
 }  // namespace qmm

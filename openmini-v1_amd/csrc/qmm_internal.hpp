@@ -40,6 +40,7 @@ namespace qmm {
 
 constexpr int kQK = 32;
 constexpr int kMaxGemvBatch = 4;  // batch rows per GEMV launch
+constexpr int kMaxGroup = 4;      // weights sharing one GEMV launch
 
 // IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
@@ -127,9 +128,16 @@ hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, fl
 // y[batch][n] = x[batch][k] . W^T for 1 <= batch <= kMaxGemvBatch.
 hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hipStream_t s);
 
+// One launch for `count` weights of equal type and K sharing x: ys[i][batch][n_i] =
+// x . W_i^T (count <= kMaxGroup); or, with swiglu, a (gate, up) pair of equal shape and
+// ys[0][batch][n] = silu(x . Wg^T) * (x . Wu^T).
+hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int count, const float* x, int batch,
+                             bool swiglu, hipStream_t s);
+
 // y[m][n] = x_bf16[m][k] . W^T.
-hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m,
-                            hipStream_t s);
+// gate_in_y: y holds gate = x . Wg^T on entry; each element becomes silu(gate) * (x . W^T).
+hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
+                            bool gate_in_y = false);
 
 // quant::dequantize semantics for every layout the library knows (F32, F16, Q4_0,
 // Q4_1, Q8_0, Q2_K..Q8_K): complete blocks of `bytes` are dequantized, the rest of the

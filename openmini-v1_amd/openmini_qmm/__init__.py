@@ -5,6 +5,8 @@ include/openmini_qmm.h); this package is its host-side mirror of the reference's
 operator interface (see ops.py) plus synthetic-input helpers (synth.py).
 """
 from ._native import LIB_PATH, Q4_0, Q8_0, QmmError, lib  # noqa: F401
+from .layer import (AttentionWeights, FFNWeights, ffn_gate_up, ffn_gate_up_bf16,  # noqa: F401
+                    gemv_multi)
 from .ops import (DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,  # noqa: F401
                   InsufficientData, InvalidInput, QuantError, QuantizedWeight, Stream,
                   UnsupportedType, dequantize, dequantize_simd, get_gemm_engine, init, linear,

@@ -166,6 +166,28 @@ def linear_bf16x_f64(qtype: int, w: np.ndarray, N: int, K: int, xb16: np.ndarray
     return y
 
 
+def silu_f64(v: np.ndarray) -> np.ndarray:
+    """silu(v) = v / (1 + exp(-v)) (model.rs:1187-1189), in fp64.  exp overflow for
+    v < -709 gives v / inf = -0.0, the limit."""
+    v = np.asarray(v, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return v / (1.0 + np.exp(-v))
+
+
+def ffn_hidden_f64(qtype: int, wg: np.ndarray, wu: np.ndarray, N: int, K: int,
+                   x: np.ndarray) -> np.ndarray:
+    """FFNWeights::forward's hidden state (model.rs:728-730):
+    silu(x . Wg^T) * (x . Wu^T), fp64."""
+    return silu_f64(linear_f64(qtype, wg, N, K, x)) * linear_f64(qtype, wu, N, K, x)
+
+
+def ffn_hidden_bf16x_f64(qtype: int, wg: np.ndarray, wu: np.ndarray, N: int, K: int,
+                         xb16: np.ndarray) -> np.ndarray:
+    """The same on bf16 activations (raw bits)."""
+    return (silu_f64(linear_bf16x_f64(qtype, wg, N, K, xb16))
+            * linear_bf16x_f64(qtype, wu, N, K, xb16))
+
+
 def cpu_asrun_linear(w_f32: np.ndarray, x: np.ndarray, scratch: np.ndarray | None,
                      transpose_copy: bool) -> np.ndarray:
     N, K = w_f32.shape

@@ -72,6 +72,16 @@ def test_host_only_validation():
     # quant::dequantize semantics: unknown layouts are refused before any device work
     assert L.openmini_qmm_dequantize_any(16, p, 64, 256, p) == _native.ERR_UNSUPPORTED
     assert L.openmini_qmm_dequantize_any(12, None, 0, 0, None) == 0
+    # layer projections: argument checks that precede any device work
+    arr = (ctypes.c_void_p * 5)()
+    assert L.openmini_qmm_gemv_multi(None, 1, p, arr, 1, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemv_multi(arr, 0, p, arr, 1, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemv_multi(arr, 5, p, arr, 1, None) == _native.ERR_INVALID_PARAM
+    assert b"count=5" in L.openmini_qmm_last_error()
+    assert L.openmini_qmm_gemv_multi(arr, 1, p, arr, 1, None) == _native.ERR_INVALID_PARAM
+    assert b"null weight" in L.openmini_qmm_last_error()
+    assert L.openmini_qmm_ffn_gate_up(None, None, p, p, 1, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_ffn_gate_up_bf16(None, None, p, p, 1, None) == _native.ERR_INVALID_PARAM
 
 
 def test_python_mirror_raises_reference_errors():

@@ -151,6 +151,22 @@ def test_gemv_nonfinite_activation(qmm, orc):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_gemv_nonfinite_row_stays_in_its_row(qmm, orc, qtype):
+    """In a batch, a non-finite activation row makes only that row's outputs
+    non-finite; the other rows match the oracle (row-wise f32 dots in the reference)."""
+    N, K = 96, 512
+    blocks = synth.weight_blocks(qtype, N, K, seed=65)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(66, (4, K), 1.0)
+    x[1, 300] = np.nan
+    x[3, 0] = -np.inf
+    y = run_gemv(qmm, w, x)
+    assert not np.any(np.isfinite(y[1])) and not np.any(np.isfinite(y[3]))
+    for r in (0, 2):
+        assert_parity(y[r:r + 1], orc.linear_f64(qtype, blocks, N, K, x[r:r + 1]), TOL, f"row {r}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_gemv_ragged_tiles(qmm, orc, qtype):
     """Rows not a multiple of 16 and blocks not a multiple of 4 (tile padding)."""
     for N, K in ((17, 32), (33, 160), (1000, 4000), (255, 4064)):

@@ -432,3 +432,32 @@ def test_safe_dequantize_q4_1_regression_generator(orc):
     m = np.float32(np.float16(np.float32(-1.0) + np.float32(0.1)))
     out = orc.dequantize(Q4_1, data, 64)
     assert out[32 + 2 * 5] == np.float32(np.float32(5) * d) + m
+
+
+def test_silu_pins(orc):
+    """silu(v) = v / (1 + exp(-v)) (model.rs:1187-1189): fixed points, the odd-part
+    identity silu(v) - silu(-v) = v, and v * expit(v) from scipy."""
+    from scipy.special import expit
+    assert orc.silu_f64(0.0) == 0.0
+    assert orc.silu_f64(1.0) == 1.0 / (1.0 + np.exp(-1.0))
+    assert orc.silu_f64(-1000.0) == 0.0 and np.signbit(orc.silu_f64(-1000.0))
+    assert orc.silu_f64(1000.0) == 1000.0
+    v = np.random.default_rng(5).normal(0.0, 4.0, 10_000)
+    np.testing.assert_allclose(orc.silu_f64(v) - orc.silu_f64(-v), v, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(orc.silu_f64(v), v * expit(v), rtol=1e-13, atol=1e-300)
+
+
+def test_ffn_hidden_composition(orc):
+    """silu(g) * u over the oracle's own linear layers: a swapped gate / up (the
+    gate * silu(up) mistake) fails it."""
+    from scipy.special import expit
+    from openmini_qmm import synth
+    N, K = 48, 256
+    wg = synth.weight_blocks(Q4_0, N, K, seed=1)
+    wu = synth.weight_blocks(Q4_0, N, K, seed=2)
+    x = synth.normal(3, (2, K), 1.0)
+    g = orc.linear_f64(Q4_0, wg, N, K, x)
+    u = orc.linear_f64(Q4_0, wu, N, K, x)
+    h = orc.ffn_hidden_f64(Q4_0, wg, wu, N, K, x)
+    np.testing.assert_allclose(h, g * expit(g) * u, rtol=1e-12)
+    assert not np.allclose(h, u * expit(u) * g, rtol=1e-3)
