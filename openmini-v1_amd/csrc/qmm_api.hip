@@ -335,12 +335,8 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
     if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
-    const qmm::Weight& w = weight->w;
-    for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
-        const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
-        hipError_t e = qmm::launch_gemv(w, d_x + b0 * w.k, d_y + b0 * w.n, nb, as_stream(stream));
-        if (e != hipSuccess) return hip_fail(e, "gemv launch");
-    }
+    hipError_t e = qmm::launch_gemv_rows(weight->w, nullptr, d_x, d_y, batch, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return ok();
 }
 
@@ -377,6 +373,14 @@ int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count,
     for (int i = 0; i < count; ++i) tiles += ws[i]->n_tiles;
     if (tiles > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "too many rows in one group");
     const int64_t k = ws[0]->k;
+    if (qmm::use_batch_kernel(*ws[0], batch)) {
+        // several rows: one batched pass per weight
+        for (int i = 0; i < count; ++i) {
+            hipError_t e = qmm::launch_gemv_rows(*ws[i], nullptr, d_x, d_ys[i], batch, as_stream(stream));
+            if (e != hipSuccess) return hip_fail(e, "gemv_multi launch");
+        }
+        return ok();
+    }
     for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
         const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
         float* ys[qmm::kMaxGroup];
@@ -406,14 +410,8 @@ int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qwei
     if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
     if (batch <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "batch=%lld must be >= 1", (long long)batch);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
-    const qmm::Weight* ws[2] = {&gate->w, &up->w};
-    const int64_t n = gate->w.n, k = gate->w.k;
-    for (int64_t b0 = 0; b0 < batch; b0 += qmm::kMaxGemvBatch) {
-        const int nb = (int)((batch - b0) < qmm::kMaxGemvBatch ? (batch - b0) : qmm::kMaxGemvBatch);
-        float* ys[2] = {d_h + b0 * n, d_h + b0 * n};
-        hipError_t e = qmm::launch_gemv_group(ws, ys, 2, d_x + b0 * k, nb, true, as_stream(stream));
-        if (e != hipSuccess) return hip_fail(e, "ffn_gate_up launch");
-    }
+    hipError_t e = qmm::launch_gemv_rows(gate->w, &up->w, d_x, d_h, batch, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "ffn_gate_up launch");
     return ok();
 }
 
@@ -445,11 +443,8 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
         return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
     }
     e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
-    for (int64_t b0 = 0; e == hipSuccess && b0 < m; b0 += qmm::kMaxGemvBatch) {
-        const int nb = (int)((m - b0) < qmm::kMaxGemvBatch ? (m - b0) : qmm::kMaxGemvBatch);
-        e = qmm::launch_gemv(w, static_cast<const float*>(dx) + b0 * w.k, static_cast<float*>(dy) + b0 * w.n,
-                             nb, nullptr);
-    }
+    if (e == hipSuccess)
+        e = qmm::launch_gemv_rows(w, nullptr, static_cast<const float*>(dx), static_cast<float*>(dy), m, nullptr);
     if (e == hipSuccess) e = hipMemcpy(y, dy, yb, hipMemcpyDeviceToHost);
     (void)hipFree(dx);
     (void)hipFree(dy);

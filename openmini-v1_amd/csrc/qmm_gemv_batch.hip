@@ -1,0 +1,352 @@
+// Batched decode GEMV: y[b, n] = sum_k x[b, k] * w[n, k] for up to 16 fp32 activation
+// rows in one pass over W, on fp16 MFMA with the batch rows as the MFMA rows.
+//
+// Replaces, per call of linear()/linear_gemm() with several rows
+// (openmini-server/src/model/inference/model.rs:1050-1064), the W^T copy plus f32
+// sgemm over weights dequantized at load.
+//
+// Arithmetic (every product exact, fp32 accumulation):
+//   * Codes are exact in fp16: Q4_0 as q - 8, Q8_0 as q.  They are built from the
+//     code bytes with the 1024 + u pattern (0x64XX is the fp16 1024 + XX, spacing 1)
+//     and one packed fp16 subtraction.
+//   * Per (batch row, 4-block group) the activations are scaled by 2^s, s chosen so
+//     the group's largest |x| lands in [2^14, 2^15), and split exactly into
+//     hi = x' with its low 13 mantissa bits cleared (11 significant bits, an fp16
+//     value) and lo = x' - hi (at most 13 bits, rounded toward zero to fp16: a
+//     relative error below 2^-20 of the element; elements below 2^-14 of the group
+//     maximum lose bits only below 2^-38 of it).  The scale is a range guard: fp16
+//     cannot hold the full fp32 exponent range.
+//   * v_mfma_f32_16x16x32_f16 covers one 32-element block: D = (hi + lo) . q in fp32
+//     for 16 batch rows x 16 weight rows.  Each block's D is scaled by its fp16 scale
+//     into a group sum; each group sum by 2^-s into the row's accumulator.
+//   * Non-finite activations propagate through the products (inf - inf and 0 * inf
+//     are NaN), so a row holding inf / NaN gets non-finite outputs in its own row only.
+//
+// MFMA operands (16 x 16 x 32): lane l = 16 kq + i holds A row i (batch row), k
+// elements 8 kq .. 8 kq + 7 of the block; B column i (weight row), the same k.  For a
+// (row tile, group) chunk that is slot (t, i) of block t, word kq (Q4_0: 8 nibbles)
+// or bytes 8 kq .. 8 kq + 7 (Q8_0): one 256 B / 512 B contiguous wave load per block.
+// D: lane l holds column l % 16, rows 4 (l / 16) .. + 3.
+//
+// Work split: a workgroup owns T consecutive row tiles (of kNW weights: a (gate, up)
+// pair runs both on the same tiles and writes silu(gate) * up, model.rs:713-735 with
+// silu at :1187-1189); its W waves split the K groups into contiguous slices and walk
+// them one group at a time, with the next group's loads (activations, then the chunks)
+// in flight while the current group is split (once for the T tiles) and multiplied.
+// The W partial sums of an output meet in LDS and are added in wave order
+// (deterministic).
+#include "qmm_internal.hpp"
+
+namespace qmm {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Two code bytes (selector bytes a, b of `u`) -> the fp16 pair (1024 + u_a, 1024 + u_b).
+__device__ __forceinline__ uint32_t magic_pair(uint32_t u, uint32_t sel) {
+    return __builtin_amdgcn_perm(0x64646464u, u, sel);
+}
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
+
+__device__ __forceinline__ uint32_t pk_sub(uint32_t v, _Float16 c) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, v) - f16x2{c, c});
+}
+
+// Q4_0 code word (elements 8 kq + i in the low nibble of byte i, 8 kq + 4 + i in the
+// high nibble; nibble = (q - 8) mod 16) -> 8 fp16 q - 8, elements in order.
+__device__ __forceinline__ f16x8 codes_q4(uint32_t w) {
+    const uint32_t u = w ^ 0x88888888u;  // nibbles q
+    const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+    uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1032.0f),
+                     pk_sub(magic_pair(hi, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1032.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
+// 8 Q8_0 codes (two words, int8) -> 8 fp16 q.
+__device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128
+    uint32_t p[4] = {pk_sub(magic_pair(u0, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u0, kSel23), (_Float16)1152.0f),
+                     pk_sub(magic_pair(u1, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u1, kSel23), (_Float16)1152.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
+// 8 scaled activations -> fp16 hi and lo parts (hi + lo = x' up to lo's rounding).
+__device__ __forceinline__ void split8(const float* v, int s, f16x8& hi, f16x8& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float a = __builtin_amdgcn_ldexpf(v[2 * j], s), b = __builtin_amdgcn_ldexpf(v[2 * j + 1], s);
+        const float ah = __uint_as_float(__float_as_uint(a) & 0xFFFFE000u);
+        const float bh = __uint_as_float(__float_as_uint(b) & 0xFFFFE000u);
+        h[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ah, bh));
+        l[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - ah, b - bh));
+    }
+    hi = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(h));
+    lo = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(l));
+}
+
+// Max over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four k quarters of A row l % 16),
+// with the gfx950 row-swap permutes (no LDS round trip).
+__device__ __forceinline__ float quarter_max(float m) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
+constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+
+// One group's operands in registers: the lane's activations of the 4 blocks and, per
+// (weight, tile) pair, its code word(s) and its column's scale of each block.
+template <bool kQ4, int kNT>
+struct Stage {
+    float x[4][8];
+    uint32_t c[kNT][4][kQ4 ? 1 : 2];
+    uint32_t sc[kNT][4];
+};
+
+// Workgroup: T row tiles of kNW weights, W waves splitting K.  A wave walks its slice
+// one group at a time with the next group's loads in flight (two register stages).
+template <bool kQ4, int T, int W, int kNW>
+__global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __restrict__ w0,
+                                                            const uint8_t* __restrict__ w1,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int n_rows, int n_tiles, int groups, int k, int batch) {
+    constexpr int kNT = kNW * T;  // (weight, tile) pairs of the workgroup
+    constexpr int kCB = kQ4 ? 16 : 32;
+    constexpr int kCodeBytes = kTileEntries * kCB;
+    constexpr int kChunk = chunk_bytes_for(kQ4);
+    // per wave: the 16 A rows' 2^-s of the current group while running, then the
+    // partial sums [W][kNT][64 lanes][4] for the reduction
+    constexpr int kRed = W * kNT * 256;
+    constexpr int kScale = W * 16;
+    __shared__ __attribute__((aligned(16))) float lds[kRed > kScale ? kRed : kScale];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 15, kq = lane >> 4;
+    const int tile0 = (int)blockIdx.x * T;
+    const int g0 = (int)((int64_t)groups * wave / W);
+    const int g1 = (int)((int64_t)groups * (wave + 1) / W);
+
+    const __amdgpu_buffer_rsrc_t w_rs0 = make_rsrc(w0, (uint32_t)n_tiles * groups * kChunk);
+    const __amdgpu_buffer_rsrc_t w_rs1 = make_rsrc(kNW == 2 ? w1 : w0, (uint32_t)n_tiles * groups * kChunk);
+    // Tiles past the last one re-read it (cache hits) and are not stored.
+    uint32_t tile_off[T];
+#pragma unroll
+    for (int i = 0; i < T; ++i) tile_off[i] = (uint32_t)min(tile0 + i, n_tiles - 1) * groups * kChunk;
+    // x: one buffer of batch * k floats; A row li reads batch row min(li, batch - 1)
+    // (rows past the batch are computed and not stored); elements past k read zero.
+    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x, (uint32_t)batch * (uint32_t)k * 4u);
+    const uint32_t x_row = (uint32_t)min(li, batch - 1) * (uint32_t)k;
+    float* my_scale = lds + wave * 16;
+
+    f32x4 acc[kNT];
+#pragma unroll
+    for (int i = 0; i < kNT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Issue group g's loads: activations first (L2 hits), then the chunks.
+    auto load = [&](Stage<kQ4, kNT>& st, int g) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t e = (uint32_t)g * 128u + t * 32u + kq * 8u;
+            const uint32_t off = e < (uint32_t)k ? (x_row + e) * 4u : 0x80000000u;
+            const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off, 0, 0));
+            const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off + 16u, 0, 0));
+            st.x[t][0] = a.x; st.x[t][1] = a.y; st.x[t][2] = a.z; st.x[t][3] = a.w;
+            st.x[t][4] = b.x; st.x[t][5] = b.y; st.x[t][6] = b.z; st.x[t][7] = b.w;
+        }
+#pragma unroll
+        for (int i = 0; i < kNT; ++i) {
+            const __amdgpu_buffer_rsrc_t rs = i / T == 0 ? w_rs0 : w_rs1;
+            const uint32_t soff = tile_off[i % T] + (uint32_t)g * kChunk;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t slot = (uint32_t)(t * kTileRows + li);
+                if constexpr (kQ4) {
+                    st.c[i][t][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, slot * kCB + kq * 4, soff, 0);
+                } else {
+                    const uint2 v = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, slot * kCB + kq * 8, soff, 0));
+                    st.c[i][t][0] = v.x;
+                    st.c[i][t][1] = v.y;
+                }
+                st.sc[i][t] = __builtin_amdgcn_raw_buffer_load_b16(rs, kCodeBytes + slot * 2, soff, 0);
+            }
+        }
+    };
+
+    // One group: the range scale and hi / lo split of the activations (shared by the
+    // kNT pairs), then per pair 4 blocks of 2 MFMAs and the scale FMAs.
+    auto compute = [&](const Stage<kQ4, kNT>& st) {
+        float m = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(st.x[t][j]));
+        m = quarter_max(m);
+        // 2^e <= m < 2^(e+1), e = biased exponent - 127; s = 14 - e
+        const int sh = 141 - (int)(__float_as_uint(m) >> 23);
+        if (kq == 0) my_scale[li] = __builtin_amdgcn_ldexpf(1.0f, -sh);
+        f16x8 ah[4], al[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) split8(st.x[t], sh, ah[t], al[t]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // 2^-s of the four A rows this lane's D values belong to (rows 4 kq .. 4 kq + 3)
+        const f32x4 rs = *reinterpret_cast<const f32x4*>(my_scale + kq * 4);
+#pragma unroll
+        for (int i = 0; i < kNT; ++i) {
+            f32x4 gs = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                f16x8 b;
+                if constexpr (kQ4)
+                    b = codes_q4(st.c[i][t][0]);
+                else
+                    b = codes_q8(st.c[i][t][0], st.c[i][t][kQ4 ? 0 : 1]);
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
+                const float ds = f16_bits_to_f32((uint16_t)st.sc[i][t]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds, gs[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(gs[r], rs[r], acc[i][r]);
+        }
+        // the next group rewrites my_scale after these reads (in-order LDS per wave)
+    };
+
+    if (g0 < g1) {  // uniform per wave
+        Stage<kQ4, kNT> sa, sb;
+        int g = g0;
+        load(sa, g);
+        // the loads past the slice end re-read its last group (cache hits) and are
+        // never consumed, so every path issues the same loads
+        while (true) {
+            load(sb, min(g + 1, g1 - 1));
+            compute(sa);
+            if (g + 1 >= g1) break;
+            load(sa, min(g + 2, g1 - 1));
+            compute(sb);
+            if (g + 2 >= g1) break;
+            g += 2;
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the unconsumed prefetch has landed
+    }
+
+    // The W K slices meet in LDS and are added in wave order.
+    __syncthreads();  // every wave is done with its scale slots
+#pragma unroll
+    for (int i = 0; i < kNT; ++i)
+        *reinterpret_cast<f32x4*>(lds + ((wave * kNT + i) * 64 + lane) * 4) = acc[i];
+    __syncthreads();
+    // output (tile i, batch row b, weight row r): lane (b / 4) * 16 + r, register b % 4
+    for (int f = (int)threadIdx.x; f < T * 256; f += 64 * W) {
+        const int i = f >> 8, b = (f >> 4) & 15, r = f & 15;
+        const int row = (tile0 + i) * kTileRows + r;
+        if (b >= batch || tile0 + i >= n_tiles || row >= n_rows) continue;
+        const int src = ((b >> 2) * 16 + r) * 4 + (b & 3);
+        float v[kNW];
+#pragma unroll
+        for (int nw = 0; nw < kNW; ++nw) {
+            v[nw] = lds[(nw * T + i) * 256 + src];
+#pragma unroll
+            for (int w = 1; w < W; ++w) v[nw] += lds[((w * kNT) + nw * T + i) * 256 + src];
+        }
+        if constexpr (kNW == 2)
+            y[(size_t)b * n_rows + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
+        else
+            y[(size_t)b * n_rows + row] = v[0];
+    }
+}
+
+template <bool kQ4, int T, int W, int kNW>
+hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch, hipStream_t s) {
+    const unsigned wgs = (unsigned)((w.n_tiles + T - 1) / T);
+    hipLaunchKernelGGL((gemv_batch_kernel<kQ4, T, W, kNW>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x, y,
+                       (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool use_batch_kernel(const Weight& w, int64_t batch) {
+    return batch >= kBatchMin && (int64_t)kBatchRows * w.k * 4 <= INT32_MAX;
+}
+
+hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, float* y, int64_t batch,
+                            hipStream_t s) {
+    if (use_batch_kernel(w, batch)) {
+        for (int64_t b0 = 0; b0 < batch; b0 += kBatchRows) {
+            const int nb = (int)(batch - b0 < kBatchRows ? batch - b0 : kBatchRows);
+            const hipError_t e =
+                launch_gemv_batch(w, up, x + b0 * w.k, y + b0 * w.n, nb, choose_batch_shape(w, nb, up), s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    for (int64_t b0 = 0; b0 < batch; b0 += kMaxGemvBatch) {
+        const int nb = (int)(batch - b0 < kMaxGemvBatch ? batch - b0 : kMaxGemvBatch);
+        const Weight* ws[2] = {&w, up};
+        float* ys[2] = {y + b0 * w.n, y + b0 * w.n};
+        const hipError_t e = launch_gemv_group(ws, ys, up ? 2 : 1, x + b0 * w.k, nb, up != nullptr, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Launch shape, measured on MI355X (Q4_0 / Q8_0, B = 8 and 16, N = 4096 ... 28672):
+// four waves per workgroup; tiles per workgroup so that the grid stays near one
+// workgroup per CU (256 row tiles -> 1, 512 -> 2, more -> 4).  More tiles share each
+// wave's activation split; more workgroups than CUs add activation re-reads.
+BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
+    (void)batch;
+    BatchShape sh{};
+    sh.t = pair || w.n_tiles <= 256 ? 1 : w.n_tiles <= 512 ? 2 : 4;
+    sh.w = w.groups >= 8 ? 4 : 1;
+    return sh;
+}
+
+template <bool kQ4, int kNW>
+static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
+                                 const BatchShape& sh, hipStream_t s) {
+#define QMM_BATCH_CASE(T_, W_)                                                            \
+    if (sh.t == T_ && sh.w == W_) return run<kQ4, T_, W_, kNW>(w, w1, x, y, batch, s);
+    // 1024-thread workgroups leave 128 registers a wave: one tile of one weight only
+    QMM_BATCH_CASE(1, 1)
+    QMM_BATCH_CASE(1, 4)
+    QMM_BATCH_CASE(1, 8)
+    if constexpr (kNW == 1) {
+        QMM_BATCH_CASE(1, 16)
+        QMM_BATCH_CASE(2, 1)
+        QMM_BATCH_CASE(2, 4)
+        QMM_BATCH_CASE(2, 8)
+        QMM_BATCH_CASE(4, 4)
+        QMM_BATCH_CASE(4, 8)
+    }
+#undef QMM_BATCH_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, float* y, int batch,
+                             const BatchShape& sh, hipStream_t s) {
+    if (batch < 1 || batch > kBatchRows) return hipErrorInvalidValue;
+    if ((int64_t)batch * w.k * 4 > INT32_MAX) return hipErrorInvalidValue;  // 31-bit x offsets
+    const bool q4 = w.type == OPENMINI_QMM_Q4_0;
+    if (up)
+        return q4 ? dispatch_batch<true, 2>(w, up->chunks, x, y, batch, sh, s)
+                  : dispatch_batch<false, 2>(w, up->chunks, x, y, batch, sh, s);
+    return q4 ? dispatch_batch<true, 1>(w, nullptr, x, y, batch, sh, s)
+              : dispatch_batch<false, 1>(w, nullptr, x, y, batch, sh, s);
+}
+
+}  // namespace qmm

@@ -39,7 +39,8 @@ struct openmini_qweight;
 namespace qmm {
 
 constexpr int kQK = 32;
-constexpr int kMaxGemvBatch = 4;  // batch rows per GEMV launch
+constexpr int kMaxGemvBatch = 4;  // batch rows per launch of the single-row-tuned GEMV
+constexpr int kBatchRows = 16;    // batch rows per launch of the batched GEMV (its MFMA rows)
 constexpr int kMaxGroup = 4;      // weights sharing one GEMV launch
 
 // IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16).
@@ -133,6 +134,27 @@ hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hip
 // ys[0][batch][n] = silu(x . Wg^T) * (x . Wu^T).
 hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int count, const float* x, int batch,
                              bool swiglu, hipStream_t s);
+
+// Batches of at least kBatchMin rows use the batched GEMV (qmm_gemv_batch.hip): from
+// five rows on, one pass over W beats the single-row kernel's launches of four rows.
+constexpr int kBatchMin = 5;
+bool use_batch_kernel(const Weight& w, int64_t batch);
+
+// y[batch][n] = x[batch][k] . W^T for any batch >= 1 (with `up`: the SwiGLU pair as in
+// launch_gemv_batch), split into launches of the kernel that suits the batch.
+hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, float* y, int64_t batch,
+                            hipStream_t s);
+
+// Batched GEMV (qmm_gemv_batch.hip): T row tiles per workgroup, W waves splitting K.
+struct BatchShape {
+    int t = 1, w = 8;
+};
+BatchShape choose_batch_shape(const Weight& w, int batch, bool pair);
+
+// y[batch][n] = x[batch][k] . W^T for 1 <= batch <= kBatchRows in one pass over W; with
+// `up`, a (gate = w, up) pair of equal shape and y = silu(x . Wg^T) * (x . Wu^T).
+hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, float* y, int batch,
+                             const BatchShape& sh, hipStream_t s);
 
 // y[m][n] = x_bf16[m][k] . W^T.
 // gate_in_y: y holds gate = x . Wg^T on entry; each element becomes silu(gate) * (x . W^T).

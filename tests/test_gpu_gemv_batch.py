@@ -1,0 +1,157 @@
+"""Batched decode GEMV (five or more activation rows: one pass over W on fp16 MFMA)
+against the fp64 oracle (model.rs:1050-1064 semantics: y = x . W^T), tolerance from
+tests/parity.py (1e-3 normwise and elementwise)."""
+import numpy as np
+import pytest
+
+from openmini_qmm import synth
+from parity import TOL, assert_parity
+
+pytestmark = pytest.mark.gpu
+Q4_0, Q8_0 = 2, 7
+
+
+def run_gemv(qmm, w, x):
+    B = x.shape[0]
+    dx = qmm.DeviceBuffer.from_numpy(np.ascontiguousarray(x))
+    dy = qmm.DeviceBuffer(B * w.n_rows * 4)
+    w.gemv(dx, dy, B)
+    return dy.download(np.float32, (B, w.n_rows))
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("N,K", [(1, 32), (37, 96), (130, 2080), (255, 4064), (1000, 4000), (4096, 4096)])
+@pytest.mark.parametrize("B", [5, 8, 16, 21, 40])
+def test_batch_parity(qmm, orc, qtype, N, K, B):
+    print(f"gemv batch type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.weight_blocks(qtype, N, K, seed=0xB000 + N + K + B)
+    x = synth.normal(0xB001 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    assert_parity(run_gemv(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} K={K} B={B}")
+
+
+@pytest.mark.parametrize("qtype,N,K,B", [
+    (Q8_0, 11008, 4096, 8),     # BASELINE config 1, batch 8
+    (Q8_0, 4096, 11008, 8),
+    (Q4_0, 8192, 8192, 16),     # config 4, 70B q-proj, batch 16
+    (Q4_0, 1024, 28672, 16),    # a slice of the 70B down-proj's K
+])
+def test_batch_baseline_shapes(qmm, orc, qtype, N, K, B):
+    print(f"gemv batch type={qtype} N={N} K={K} B={B}", flush=True)
+    sigma = 0.015 if K >= 8192 else 0.02
+    blocks = synth.weight_blocks(qtype, N, K, seed=0xB100 + N + B, sigma=sigma)
+    x = synth.normal(0xB101 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    print(assert_parity(run_gemv(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, "baseline"))
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_batch_rows_independent(qmm, qtype):
+    """A row's result does not depend on the other rows of the batch (each MFMA row
+    and each range scale belongs to one activation row): rows 8..15 of a 16-row call
+    equal an 8-row call of the same rows bit for bit, and a repeated call is bitwise
+    identical."""
+    N, K = 777, 2048
+    blocks = synth.weight_blocks(qtype, N, K, seed=0xB200)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(0xB201, (16, K), 1.0)
+    x[3] *= 1e6  # a loud neighbour must not change the quiet rows
+    y16 = run_gemv(qmm, w, x)
+    y8 = run_gemv(qmm, w, x[8:])
+    assert np.array_equal(y16[8:].view(np.uint32), y8.view(np.uint32))
+    assert np.array_equal(y16.view(np.uint32), run_gemv(qmm, w, x).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_batch_activation_dynamic_range(qmm, orc, qtype):
+    """Per (row, group) range scales: outliers (x1e4), tiny rows (x1e-30 with
+    subnormals), huge rows (x1e30), zero rows and zero blocks stay within the contract."""
+    N, K = 512, 4096
+    blocks = synth.weight_blocks(qtype, N, K, seed=0xB300)
+    x = synth.normal(0xB301, (8, K), 1.0)
+    x[0, 5] *= 1e4
+    x[0, 1000:1032] *= 1e-6
+    x[0, 2048:2080] = 0.0
+    x[1, :] *= 1e-30
+    x[1, 100:110] = np.float32(1e-41)  # subnormal
+    x[2, :] *= 1e30
+    x[3, :] = 0.0
+    x[4, ::64] *= 1e-20
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y = run_gemv(qmm, w, x)
+    ref = orc.linear_f64(qtype, blocks, N, K, x)
+    for r in range(8):
+        if r == 3:
+            assert np.all(y[3] == 0.0)
+            continue
+        assert_parity(y[r:r + 1], ref[r:r + 1], TOL, f"row {r}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_batch_nonfinite_row_stays_in_its_row(qmm, orc, qtype):
+    N, K = 96, 512
+    blocks = synth.weight_blocks(qtype, N, K, seed=0xB400)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(0xB401, (8, K), 1.0)
+    x[1, 300] = np.nan
+    x[3, 0] = -np.inf
+    x[6, 511] = np.inf
+    y = run_gemv(qmm, w, x)
+    for r in (1, 3, 6):
+        assert not np.any(np.isfinite(y[r])), r
+    for r in (0, 2, 4, 5, 7):
+        assert_parity(y[r:r + 1], orc.linear_f64(qtype, blocks, N, K, x[r:r + 1]), TOL, f"row {r}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("N,K,B", [(11008, 4096, 8), (1000, 2080, 16), (40, 96, 5)])
+def test_batch_ffn_gate_up(qmm, orc, qtype, N, K, B):
+    """FFN hidden state silu(x . Wg^T) * (x . Wu^T) (model.rs:713-735) for a batch: the
+    pair kernel's gate and up sums are the single-weight batched GEMV's bit for bit."""
+    print(f"ffn_gate_up batch type={qtype} N={N} K={K} B={B}", flush=True)
+    bg = synth.weight_blocks(qtype, N, K, seed=0xB500 + N)
+    bu = synth.weight_blocks(qtype, N, K, seed=0xB501 + N)
+    wg, wu = qmm.QuantizedWeight(qtype, bg, N, K), qmm.QuantizedWeight(qtype, bu, N, K)
+    x = synth.normal(0xB502 + B, (B, K), 1.0)
+    dx, dh = qmm.DeviceBuffer.from_numpy(x), qmm.DeviceBuffer(B * N * 4)
+    qmm.ffn_gate_up(wg, wu, dx, dh, B)
+    h = dh.download(np.float32, (B, N))
+    assert_parity(h, orc.ffn_hidden_f64(qtype, bg, bu, N, K, x), TOL, "hidden")
+    g = run_gemv(qmm, wg, x).astype(np.float64)
+    u = run_gemv(qmm, wu, x).astype(np.float64)
+    np.testing.assert_allclose(h, orc.silu_f64(g) * u, rtol=1e-5, atol=1e-6 * float(np.max(np.abs(h))))
+
+
+def test_batch_gemv_multi(qmm, orc):
+    """gemv_multi with a batch runs one batched pass per weight."""
+    shapes = ((4096, 4096), (1024, 4096), (1024, 4096))
+    B = 12
+    ws, blocks = [], []
+    for i, (n, k) in enumerate(shapes):
+        b = synth.weight_blocks(Q4_0, n, k, seed=0xB600 + i)
+        blocks.append(b)
+        ws.append(qmm.QuantizedWeight(Q4_0, b, n, k))
+    x = synth.normal(0xB610, (B, 4096), 1.0)
+    dx = qmm.DeviceBuffer.from_numpy(x)
+    dys = [qmm.DeviceBuffer(B * w.n_rows * 4) for w in ws]
+    qmm.gemv_multi(ws, dx, dys, B)
+    for i, (w, b, dy) in enumerate(zip(ws, blocks, dys)):
+        y = dy.download(np.float32, (B, w.n_rows))
+        assert_parity(y, orc.linear_f64(Q4_0, b, w.n_rows, 4096, x), TOL, f"weight {i}")
+        assert np.array_equal(y.view(np.uint32), run_gemv(qmm, w, x).view(np.uint32))
+
+
+def test_batch_linearity_full_size(qmm):
+    """Size-independent property at the 70B gate shape with 16 rows: y(2 x1 + x2) =
+    2 y(x1) + y(x2) within fp32 reassociation, and zero rows give exact zeros."""
+    N, K = 28672, 8192
+    print(f"gemv batch linearity N={N} K={K}", flush=True)
+    blocks = synth.weight_blocks(Q4_0, N, K, seed=0xB700, sigma=0.015)
+    w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
+    x1 = synth.normal(0xB701, (16, K), 1.0)
+    x2 = synth.normal(0xB702, (16, K), 1.0)
+    y1, y2 = run_gemv(qmm, w, x1), run_gemv(qmm, w, x2)
+    y12 = run_gemv(qmm, w, (np.float32(2.0) * x1 + x2).astype(np.float32))
+    p = assert_parity(y12, 2.0 * y1.astype(np.float64) + y2, TOL, "linearity")
+    assert p["normwise"] <= 2e-6, p
+    assert np.all(run_gemv(qmm, w, np.zeros((16, K), np.float32)) == 0.0)
