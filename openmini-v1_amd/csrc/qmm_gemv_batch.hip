@@ -25,7 +25,12 @@
 // MFMA operands (16 x 16 x 32): lane l = 16 kq + i holds A row i (batch row), k
 // elements 8 kq .. 8 kq + 7 of the block; B column i (weight row), the same k.  For a
 // (row tile, group) chunk that is slot (t, i) of block t, word kq (Q4_0: 8 nibbles)
-// or bytes 8 kq .. 8 kq + 7 (Q8_0): one 256 B / 512 B contiguous wave load per block.
+// or bytes 8 kq .. 8 kq + 7 (Q8_0).  A chunk arrives as in the single-row kernel --
+// lane l reads slot l whole, one 1 KB (Q4_0) / 2 KB (Q8_0) wave load plus its 128 B
+// of scales -- and a 4 x 4 register transpose across the wave's four 16-lane rows
+// (row swaps, no LDS) hands every lane its words of all four blocks.  Vector-memory
+// instructions are what limits this kernel (each costs the address unit about the
+// same whatever its width), so wide loads and register shuffles beat narrow loads.
 // D: lane l holds column l % 16, rows 4 (l / 16) .. + 3.
 //
 // Work split: a workgroup owns T consecutive row tiles (of kNW weights: a (gate, up)
@@ -103,13 +108,40 @@ __device__ __forceinline__ float quarter_max(float m) {
 // s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
+// Register transposes across the four 16-lane rows of a wave (gfx950 row swaps:
+// permlane32_swap exchanges rows 2, 3 of its first operand with rows 0, 1 of its
+// second; permlane16_swap rows 1, 3 of the first with rows 0, 2 of the second).
+// transpose4: register j of row r becomes register r of row j.
+__device__ __forceinline__ void transpose4(uint32_t& a0, uint32_t& a1, uint32_t& a2, uint32_t& a3) {
+    const auto p = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+    const auto q = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+    const auto u = __builtin_amdgcn_permlane16_swap(p[0], q[0], false, false);
+    const auto v = __builtin_amdgcn_permlane16_swap(p[1], q[1], false, false);
+    a0 = u[0];
+    a1 = u[1];
+    a2 = v[0];
+    a3 = v[1];
+}
+
+// broadcast4: out[t] holds row t of v in every row.
+__device__ __forceinline__ void broadcast4(float v, float* out) {
+    const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const auto a = __builtin_amdgcn_permlane32_swap(h[0], h[0], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(h[1], h[1], false, false);
+    out[0] = __uint_as_float(a[0]);
+    out[1] = __uint_as_float(b[0]);
+    out[2] = __uint_as_float(a[1]);
+    out[3] = __uint_as_float(b[1]);
+}
+
 // One group's operands in registers: the lane's activations of the 4 blocks and, per
-// (weight, tile) pair, its code word(s) and its column's scale of each block.
+// (weight, tile) pair, chunk slot `lane` (block lane / 16, row lane % 16) -- its codes
+// and scale, one wide load each -- later transposed to the MFMA lanes.
 template <bool kQ4, int kNT>
 struct Stage {
     float x[4][8];
-    uint32_t c[kNT][4][kQ4 ? 1 : 2];
-    uint32_t sc[kNT][4];
+    uint4 c[kNT][kQ4 ? 1 : 2];
+    uint32_t sc[kNT];
 };
 
 // Workgroup: T row tiles of kNW weights, W waves splitting K.  A wave walks its slice
@@ -167,19 +199,11 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         for (int i = 0; i < kNT; ++i) {
             const __amdgpu_buffer_rsrc_t rs = i / T == 0 ? w_rs0 : w_rs1;
             const uint32_t soff = tile_off[i % T] + (uint32_t)g * kChunk;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t slot = (uint32_t)(t * kTileRows + li);
-                if constexpr (kQ4) {
-                    st.c[i][t][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, slot * kCB + kq * 4, soff, 0);
-                } else {
-                    const uint2 v = __builtin_bit_cast(
-                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, slot * kCB + kq * 8, soff, 0));
-                    st.c[i][t][0] = v.x;
-                    st.c[i][t][1] = v.y;
-                }
-                st.sc[i][t] = __builtin_amdgcn_raw_buffer_load_b16(rs, kCodeBytes + slot * 2, soff, 0);
-            }
+            st.c[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * kCB, soff, 0));
+            if constexpr (!kQ4)
+                st.c[i][1] =
+                    __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * kCB + 16, soff, 0));
+            st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, kCodeBytes + lane * 2, soff, 0);
         }
     };
 
@@ -205,19 +229,32 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         const f32x4 rs = *reinterpret_cast<const f32x4*>(my_scale + kq * 4);
 #pragma unroll
         for (int i = 0; i < kNT; ++i) {
+            // lane (kq, i) takes word kq (Q4_0) / words 2 kq, 2 kq + 1 (Q8_0) of slot
+            // (t, i) for t = 0..3, and the scales of its column
+            uint32_t e[4], o[4];
+            if constexpr (kQ4) {
+                e[0] = st.c[i][0].x; e[1] = st.c[i][0].y; e[2] = st.c[i][0].z; e[3] = st.c[i][0].w;
+                transpose4(e[0], e[1], e[2], e[3]);
+            } else {
+                e[0] = st.c[i][0].x; o[0] = st.c[i][0].y; e[1] = st.c[i][0].z; o[1] = st.c[i][0].w;
+                e[2] = st.c[i][1].x; o[2] = st.c[i][1].y; e[3] = st.c[i][1].z; o[3] = st.c[i][1].w;
+                transpose4(e[0], e[1], e[2], e[3]);
+                transpose4(o[0], o[1], o[2], o[3]);
+            }
+            float ds[4];
+            broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
             f32x4 gs = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 f16x8 b;
                 if constexpr (kQ4)
-                    b = codes_q4(st.c[i][t][0]);
+                    b = codes_q4(e[t]);
                 else
-                    b = codes_q8(st.c[i][t][0], st.c[i][t][kQ4 ? 0 : 1]);
+                    b = codes_q8(e[t], o[t]);
                 f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
-                const float ds = f16_bits_to_f32((uint16_t)st.sc[i][t]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds, gs[r]);
+                for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds[t], gs[r]);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(gs[r], rs[r], acc[i][r]);
@@ -304,14 +341,16 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
     return hipSuccess;
 }
 
-// Launch shape, measured on MI355X (Q4_0 / Q8_0, B = 8 and 16, N = 4096 ... 28672):
+// Launch shape, measured on MI355X (Q4_0 / Q8_0, B = 4, 8, 16, N = 4096 ... 28672):
 // four waves per workgroup; tiles per workgroup so that the grid stays near one
-// workgroup per CU (256 row tiles -> 1, 512 -> 2, more -> 4).  More tiles share each
-// wave's activation split; more workgroups than CUs add activation re-reads.
+// workgroup per CU (256 row tiles -> 1, 512 -> 2, 1024 -> 4, more -> 8; Q8_0 at most
+// 4, whose 8-tile registers would leave one wave per SIMD).  More tiles share each
+// wave's activation loads and split; more workgroups than CUs add activation re-reads.
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     (void)batch;
     BatchShape sh{};
-    sh.t = pair || w.n_tiles <= 256 ? 1 : w.n_tiles <= 512 ? 2 : 4;
+    const bool q4 = w.type == OPENMINI_QMM_Q4_0;
+    sh.t = pair || w.n_tiles <= 256 ? 1 : w.n_tiles <= 512 ? 2 : (w.n_tiles <= 1024 || !q4) ? 4 : 8;
     sh.w = w.groups >= 8 ? 4 : 1;
     return sh;
 }
@@ -332,6 +371,9 @@ static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float
         QMM_BATCH_CASE(2, 8)
         QMM_BATCH_CASE(4, 4)
         QMM_BATCH_CASE(4, 8)
+        if constexpr (kQ4) {
+            QMM_BATCH_CASE(8, 4)
+        }
     }
 #undef QMM_BATCH_CASE
     return hipErrorInvalidValue;
