@@ -287,6 +287,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--no-layer", action="store_true", help="skip the decode-layer leg")
+    ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode legs")
     ap.add_argument("--eager", action="store_true",
                     help="launch directly instead of replaying a HIP graph (for counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -321,6 +322,18 @@ def main(argv=None) -> int:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
         log(f"decode layer: grouped {layer['grouped_us']:.2f} us ({layer['grouped_gbs']:.1f} GB/s), "
             f"separate {layer['separate_us']:.2f} us ({layer['separate_gbs']:.1f} GB/s)")
+    batched = []
+    if not args.no_batch:
+        # BASELINE configs[1] (Q8_0, batch 8) and configs[4] (70B gate, batch 16)
+        for qtype, n, k, b, seed in ((Q8_0, 11008, 4096, 8, 0x5EED0011), (Q4_0, 28672, 8192, 16, 0x5EED0041)):
+            r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
+                           qtype=qtype, batch=b, seed=seed)
+            name = "q4_0" if qtype == Q4_0 else "q8_0"
+            batched.append({"workload": f"{name}_gemv_n{n}_k{k}_b{b}", "unit": "GB/s",
+                            "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                            "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
+                            "alg_bytes_per_step": r["alg_bytes_per_step"]})
+            log(f"batched {batched[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
     copy = None
     if args.calibrate_copy:
         copy = copy_calibration(qmm, hipr, stream)
@@ -369,6 +382,8 @@ def main(argv=None) -> int:
                          "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
                          "kernel_us": round(gemm["kernel_ms"] * 1e3, 3)},
         }
+    if batched:
+        out["batched_decode"] = batched
     if layer:
         out["decode_layer"] = {
             "workload": "q4_0_llama7b_layer_7proj_b1", "unit": "GB/s",

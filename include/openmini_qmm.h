@@ -139,8 +139,9 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
  * gemm_engine.rs:40), on the quantized W without materialising f32 weights. */
 
 /* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
- * Any batch >= 1; launches cover 4 activation rows each (weights are read once
- * per launch), so batches above 4 re-read W once per 4 rows.
+ * Any batch >= 1.  Up to 4 rows: the single-row-tuned kernel (one launch per 4
+ * rows); 5 or more: the batched kernel, one pass over W per 16 rows, in which a
+ * row's result does not depend on the other rows of the call.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);
@@ -153,17 +154,20 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
 
 /* ---- projections of one layer (src/model/inference/model.rs) ----------------------- */
 
-/* Weights that share the input in one launch per 4 batch rows: d_ys[i][batch, N_i] =
- * x[batch, K] . W_i^T for i < count (1..4), all of one type and one K.  Replaces the
- * three linear_gemm calls of prepare_qkv (model.rs:1392-1394: q, k, v of one
- * normalised hidden state).  d_x must be 16-byte aligned. */
+/* Weights that share the input: d_ys[i][batch, N_i] = x[batch, K] . W_i^T for
+ * i < count (1..4), all of one type and one K; one launch per 4 batch rows, or from
+ * 5 rows on one batched pass per weight (results identical to openmini_qmm_gemv of
+ * each weight).  Replaces the three linear_gemm calls of prepare_qkv
+ * (model.rs:1392-1394: q, k, v of one normalised hidden state).  d_x must be
+ * 16-byte aligned. */
 int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count, const float* d_x,
                             float* const* d_ys, int64_t batch, void* stream);
 
 /* FFN hidden state of FFNWeights::forward (model.rs:728-731, the silu(gate) * up
  * branch; silu(v) = v / (1 + exp(-v)), model.rs:1187-1189):
  * d_h[batch, N] = silu(x . Wg^T) * (x . Wu^T), gate and up of one type and shape, one
- * launch per 4 batch rows reading both weights.  d_x must be 16-byte aligned. */
+ * launch reading both weights per 4 batch rows (per 16 rows from 5 rows on).  d_x
+ * must be 16-byte aligned. */
 int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qweight_t* up,
                              const float* d_x, float* d_h, int64_t batch, void* stream);
 
