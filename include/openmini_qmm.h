@@ -95,6 +95,15 @@ int openmini_qmm_init(int device);
 /* Message of the last failing call on this thread ("" if none). */
 const char* openmini_qmm_last_error(void);
 
+/* Log sink (native/include/openmini.h:151-155, openmini_set_log_callback): every
+ * failure recorded for openmini_qmm_last_error() is also passed to `callback` as
+ * (OPENMINI_QMM_LOG_ERROR, message, user_data), on the failing thread, after the
+ * library's own state is updated; callbacks must not call back into the library.
+ * A null callback turns logging off.  Process-wide; safe to call from any thread. */
+#define OPENMINI_QMM_LOG_ERROR 3
+typedef void (*openmini_qmm_log_callback_t)(int level, const char* text, void* user_data);
+int openmini_qmm_set_log_callback(openmini_qmm_log_callback_t callback, void* user_data);
+
 /* GpuQuantOps::is_available (src/model/inference/quant_simd.rs:2979): 1 when a
  * gfx950 device is usable, else 0.  Never fails. */
 int openmini_qmm_is_available(void);

@@ -22,6 +22,23 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// The log sink of openmini_qmm_set_log_callback (callback and its user data change
+// together under the mutex; the call itself runs outside it).
+std::mutex g_log_mu;
+openmini_qmm_log_callback_t g_log_cb = nullptr;
+void* g_log_user = nullptr;
+
+void log_error(const char* msg) {
+    openmini_qmm_log_callback_t cb;
+    void* user;
+    {
+        std::lock_guard<std::mutex> lk(g_log_mu);
+        cb = g_log_cb;
+        user = g_log_user;
+    }
+    if (cb) cb(OPENMINI_QMM_LOG_ERROR, msg, user);
+}
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -29,6 +46,7 @@ int fail(int code, const char* fmt, ...) {
     vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
     g_last_error = buf;
+    log_error(buf);
     return code;
 }
 
@@ -234,6 +252,15 @@ int openmini_qmm_init(int device) {
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
     int rc = ensure_device(nullptr);
     if (rc != OPENMINI_QMM_OK) return rc;
+    return ok();
+}
+
+int openmini_qmm_set_log_callback(openmini_qmm_log_callback_t callback, void* user_data) {
+    {
+        std::lock_guard<std::mutex> lk(g_log_mu);
+        g_log_cb = callback;
+        g_log_user = user_data;
+    }
     return ok();
 }
 

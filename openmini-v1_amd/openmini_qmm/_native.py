@@ -66,11 +66,16 @@ _i = ctypes.c_int
 _i64 = ctypes.c_int64
 _sz = ctypes.c_size_t
 
+# void (*)(int level, const char* text, void* user_data)
+LOG_CALLBACK = ctypes.CFUNCTYPE(None, ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
+LOG_ERROR = 3
+
 # name -> (restype, argtypes); mirrors include/openmini_qmm.h one to one.
 SIGNATURES = {
     "openmini_qmm_version": (ctypes.c_char_p, []),
     "openmini_qmm_init": (_i, [_i]),
     "openmini_qmm_last_error": (ctypes.c_char_p, []),
+    "openmini_qmm_set_log_callback": (_i, [LOG_CALLBACK, _p]),
     "openmini_qmm_is_available": (_i, []),
     "openmini_qmm_device_info": (_i, [ctypes.c_char_p, _sz]),
     "openmini_qmm_required_bytes": (_i, [_i, _sz, ctypes.POINTER(_sz)]),

@@ -96,3 +96,30 @@ def test_python_mirror_raises_reference_errors():
         safe_dequantize(bytes(30), 3, 64)
     assert (ei.value.expected, ei.value.actual) == (40, 30)
     assert safe_dequantize_q4_0(b"", 0).size == 0
+
+
+def test_log_callback_receives_every_failure():
+    """openmini_set_log_callback semantics (native/include/openmini.h:151-155): the
+    sink sees each failure's message with its user data; a null sink stops it."""
+    from openmini_qmm import _native
+    L = _native.lib()
+    seen = []
+
+    @_native.LOG_CALLBACK
+    def sink(level, text, user):
+        seen.append((level, text.decode(), user))
+
+    assert L.openmini_qmm_set_log_callback(sink, ctypes.c_void_p(1234)) == 0
+    try:
+        out = ctypes.c_size_t()
+        assert L.openmini_qmm_required_bytes(16, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
+        h = ctypes.c_void_p()
+        assert L.openmini_qmm_upload(2, None, 0, 1, 48, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
+    finally:
+        assert L.openmini_qmm_set_log_callback(_native.LOG_CALLBACK(), None) == 0
+    assert len(seen) == 2, seen
+    assert all(lv == _native.LOG_ERROR and u == 1234 for lv, _, u in seen)
+    assert "16" in seen[0][1]  # the unsupported type id
+    assert "multiple of 32" in seen[1][1]
+    assert L.openmini_qmm_required_bytes(16, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
+    assert len(seen) == 2  # logging is off again
