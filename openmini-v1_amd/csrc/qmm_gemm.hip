@@ -12,15 +12,15 @@
 // MFMA takes, so the kernel keeps both busy: two waves per SIMD, MFMA results in
 // VGPRs, and each MFMA issued before the FMAs of the previous one.
 //
-// Tiling: a 512-thread workgroup computes a 128 x 192 tile of y (12 weight tiles).
-// Its 8 waves are 4 column slices x 2 K halves; a wave owns 128 rows x 48 columns
-// (3 weight tiles: 8 x 3 MFMA subtiles, 96 fp32 accumulators per lane) over one
-// half of K, and the two halves are added through LDS at the end (fixed order).
-// A K step is one 4-block group (128 elements):
-//   * x: each K half's 128 x 128 bf16 slab is copied HBM -> LDS by buffer loads
-//     with an LDS destination (no registers), double-buffered, rows XOR-swizzled in
+// Tiling: a workgroup computes a kBM x (48 kNW) tile of y with kNW column slices x
+// kKS K parts of waves (launch_kind picks 128 x 96 with 2 x 2 waves, or 64 x 96
+// with 2 x 4 waves for M <= 128).  A wave owns kBM rows x 48 columns (3 weight tiles:
+// kBM/16 x 3 MFMA subtiles of fp32 accumulators) over one K part, and the parts are
+// added through LDS at the end (fixed order).  A K step is two blocks (64 elements):
+//   * x: each K part's kBM x 64 bf16 slab is copied HBM -> LDS by buffer loads with
+//     an LDS destination (no registers), double-buffered, rows XOR-swizzled in
 //     16-byte segments so the A-fragment reads are bank-conflict free;
-//   * weights: each wave loads its 3 chunks' codes and scales straight into
+//   * weights: each wave loads its 3 tiles' codes and scales straight into
 //     registers two K steps ahead (three register sets: first-touch weights come
 //     from HBM, whose latency under load exceeds one step) and converts its own B
 //     fragments (its columns are its own, so nothing is converted twice).
@@ -32,9 +32,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;  // x rows per workgroup
+constexpr int kBMMax = 128;  // most x rows per workgroup
 constexpr int kWT = 3;    // weight tiles (16 columns each) per wave
-constexpr int kMI = kBM / 16;  // MFMA row subtiles per wave
 
 __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     // bf16 of exactly-representable values = high halves of their fp32 bits.
@@ -87,9 +86,11 @@ struct BRegs {
 // s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
-// Workgroup shape: kNW column slices x kKS K parts of waves; a K step is kSB blocks.
-template <int kNW, int kKS, int kSB>
+// Workgroup shape: kBM x rows, kNW column slices x kKS K parts of waves; a K step is
+// kSB blocks.
+template <int kBM, int kNW, int kKS, int kSB>
 struct Shape {
+    static constexpr int kMI = kBM / 16;                   // MFMA row subtiles per wave
     static constexpr int kThreads = 64 * kNW * kKS;
     static constexpr int kBT = kNW * kWT;                 // weight tiles per workgroup
     static constexpr int kRowB = kSB * kQK * 2;            // bytes of one x row per step
@@ -105,11 +106,12 @@ struct Shape {
 
 // kGate: y holds the gate projection on entry and each element is replaced by
 // silu(gate) * (x . W^T), silu(v) = v / (1 + exp(-v)) (model.rs:713-735, :1187-1189).
-template <bool kQ4, int kNW, int kKS, int kSB, bool kGate>
+template <bool kQ4, int kBM, int kNW, int kKS, int kSB, bool kGate>
 __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ chunks, float* __restrict__ y,
     int m_rows, int n_rows, int n_tiles, int groups, int k) {
-    using S = Shape<kNW, kKS, kSB>;
+    using S = Shape<kBM, kNW, kKS, kSB>;
+    constexpr int kMI = S::kMI;
     constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kChunk = chunk_bytes_for(kQ4);
     constexpr int kStepsPerGroup = kTileBlocks / kSB;
@@ -321,24 +323,26 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     }
 }
 
-template <bool kQ4, int kNW, int kKS, int kSB, bool kGate>
+template <bool kQ4, int kBM, int kNW, int kKS, int kSB, bool kGate>
 hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
-    using S = Shape<kNW, kKS, kSB>;
+    using S = Shape<kBM, kNW, kKS, kSB>;
     const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL((gemm_kernel<kQ4, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
+    hipLaunchKernelGGL((gemm_kernel<kQ4, kBM, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
                        (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     return hipGetLastError();
 }
 
-// Shape by the number of 128-row blocks of x: one -> 1 column slice x 4 K parts
-// (tile 128 x 48, one workgroup per CU), more -> 2 column slices x 2 K halves (tile
-// 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers overlap the other's
-// work).  Measured on MI355X against 4 x 2 (128 x 192) with 2- and 4-block K steps:
-// equal or faster on Q8_0 11008 x 4096 at M = 128 / 512 / 2048.
+// Shape by M.  Up to 128 rows: 64-row tiles, 2 column slices x 4 K parts (tile
+// 64 x 96, 512 threads, 72 KB of LDS) -- twice the workgroups of 128-row tiles where
+// too few of them would fill the CUs.  More rows: 128-row tiles, 2 column slices x 2
+// K halves (tile 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers
+// overlap the other's work).  Measured on MI355X, Q8_0 11008 x 4096: M = 128 29.8 us
+// (128 x 48 tiles with 4 K parts: 35.6 us); M = 256 / 512 / 2048 against 64-row tiles
+// and 4 x 2 (128 x 192) tiles: equal or faster.
 template <bool kQ4, bool kGate>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
-    if (m <= kBM) return launch_shape<kQ4, 1, 4, 2, kGate>(w, x, y, m, s);
-    return launch_shape<kQ4, 2, 2, 2, kGate>(w, x, y, m, s);
+    if (m <= kBMMax) return launch_shape<kQ4, 64, 2, 4, 2, kGate>(w, x, y, m, s);
+    return launch_shape<kQ4, 128, 2, 2, 2, kGate>(w, x, y, m, s);
 }
 
 }  // namespace
@@ -346,7 +350,7 @@ hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, 
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
                             bool gate_in_y) {
     // x offsets are 32-bit: launches cover row ranges whose x is below 2 GiB.
-    const int64_t rows_per_launch = ((((int64_t)1 << 31) - 1) / (w.k * 2)) / kBM * kBM;
+    const int64_t rows_per_launch = ((((int64_t)1 << 31) - 1) / (w.k * 2)) / kBMMax * kBMMax;
     if (rows_per_launch <= 0) return hipErrorInvalidValue;  // one row tile of x exceeds 2 GiB
     for (int64_t m_off = 0; m_off < m; m_off += rows_per_launch) {
         const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
