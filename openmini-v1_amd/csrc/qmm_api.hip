@@ -155,13 +155,6 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     return OPENMINI_QMM_OK;
 }
 
-// Zeroes the tile padding (rows past n, blocks past nb) before the repack fills
-// the rest; nothing to do when the shape tiles exactly.
-hipError_t clear_padding(const qmm::Weight& w, hipStream_t s) {
-    if (w.n % qmm::kTileRows == 0 && w.nb % qmm::kTileBlocks == 0) return hipSuccess;
-    return hipMemsetAsync(w.chunks, 0, w.device_bytes, s);
-}
-
 int check_weight(const openmini_qweight* h) {
     if (!h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null weight handle");
     int dev = 0;
@@ -205,7 +198,6 @@ int upload_from_host(int type, const void* host_blocks, size_t bytes, int64_t n_
     }
     hipStream_t s = as_stream(stream);
     e = hipMemcpyAsync(staging, host_blocks, need, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = clear_padding(h->w, s);
     if (e == hipSuccess) e = launch_repack(h->w, static_cast<const uint8_t*>(staging), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     (void)hipFree(staging);
@@ -319,9 +311,7 @@ int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_
     openmini_qweight* h = nullptr;
     rc = alloc_weight(type, n_rows, k_cols, dev, &h);
     if (rc != OPENMINI_QMM_OK) return rc;
-    hipError_t e = clear_padding(h->w, as_stream(stream));
-    if (e == hipSuccess)
-        e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(d_gguf_blocks), as_stream(stream));
+    hipError_t e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(d_gguf_blocks), as_stream(stream));
     if (e != hipSuccess) {
         openmini_qmm_free_weight(h);
         return hip_fail(e, "repack launch");

@@ -115,8 +115,8 @@ struct Weight {
 
 // ---- kernel launchers (qmm_repack.hip, qmm_gemv.hip, qmm_gemm.hip) ----------------
 
-// GGUF blocks (device, row-major [n][nb]) -> the chunks of `w` (whose padding the
-// caller has zeroed).
+// GGUF blocks (device, row-major [n][nb]) -> the chunks of `w`, every byte written
+// (the tile padding as zeros).
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s);
 
 // Repacked weight -> f32 [n][k].

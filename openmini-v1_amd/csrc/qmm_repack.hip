@@ -13,71 +13,90 @@
 namespace qmm {
 namespace {
 
-constexpr int kTile = 256;  // GGUF blocks per workgroup in the repack
+constexpr int kRepackChunks = 4;  // consecutive chunks (of one row tile) per repack workgroup
+constexpr int kRepackThreads = kRepackChunks * kTileEntries;  // one thread per chunk slot
 
 __device__ __forceinline__ uint32_t q4_code(const uint8_t* qs, int e) {
     uint8_t b = qs[e >> 1];
     return (e & 1) ? (b & 0x0Fu) : (b >> 4);
 }
 
-// One workgroup repacks kTile consecutive GGUF blocks (row-major order).  Full
-// tiles of a 16-byte aligned source are staged through LDS with 16-byte loads (a
-// tile is 4608 B for Q4_0 and 8704 B for Q8_0, both multiples of 16); the last
-// partial tile and unaligned sources fall back to byte loads.  Each block's codes
-// (16 / 32 B) and scale then go to its slot of its chunk.
+// One workgroup writes kRepackChunks consecutive chunks of one row tile, whole: thread
+// t fills slot e = t % 64 of chunk t / 64 -- block 4 g + e / 16 of row 16 rt + e % 16 --
+// so each chunk's codes and scales leave as contiguous wave stores.  Slots outside the
+// weight (rows past n, blocks past nb: the tile padding) are written as zeros, so every
+// byte of the chunk array is written exactly once and no clearing pass is needed.
+// The workgroup's 16 rows x 16 blocks of GGUF bytes are staged through LDS with 16-byte
+// loads when they are all present and 16-byte aligned (nb % 8 == 0, aligned source);
+// otherwise each thread reads its own block with byte loads.
 template <int kBPB>
-__global__ __launch_bounds__(kTile) void repack_kernel(const uint8_t* __restrict__ gguf,
-                                                       int64_t nblocks, int64_t nb, int64_t groups,
-                                                       int aligned16, uint8_t* __restrict__ chunks) {
+__global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* __restrict__ gguf, int64_t n,
+                                                                int64_t nb, int64_t groups, int64_t quads,
+                                                                int aligned16, uint8_t* __restrict__ chunks) {
     constexpr bool kQ4 = kBPB == 18;
     constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kChunk = chunk_bytes_for(kQ4);
-    __shared__ uint4 tile[kTile * kBPB / 16];
+    constexpr int kRowB = kRepackChunks * kTileBlocks * kBPB;  // one row's bytes in the workgroup
+    constexpr int kPieces = kTileRows * kRowB / 16;
+    __shared__ uint4 tile[kPieces];
     uint8_t* t8 = reinterpret_cast<uint8_t*>(tile);
-    const int64_t blk0 = (int64_t)blockIdx.x * kTile;
-    const int64_t left = nblocks - blk0;
-    const int nblk = left < kTile ? (int)left : kTile;
-    const uint8_t* src = gguf + blk0 * kBPB;
-    if (nblk == kTile && aligned16) {
-        const uint4* s4 = reinterpret_cast<const uint4*>(src);
-        for (int i = threadIdx.x; i < kTile * kBPB / 16; i += kTile) tile[i] = s4[i];
-    } else {
-        for (int i = threadIdx.x; i < nblk * kBPB; i += kTile) t8[i] = src[i];
-    }
-    __syncthreads();
-    const int t = threadIdx.x;
-    if (t >= nblk) return;
-    const uint8_t* b = t8 + t * kBPB;
-    const int64_t g = blk0 + t;
-    const int64_t row = g / nb, blk = g % nb;
-    uint8_t* chunk = chunks + chunk_of(row, blk, groups) * kChunk;
-    const int e = slot_of(row, blk);
-    reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = (uint16_t)(b[0] | (b[1] << 8));
-    const uint8_t* qs = b + 2;
-    if constexpr (kQ4) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t v = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t lo = q4_code(qs, 8 * j + i);
-                uint32_t hi = q4_code(qs, 8 * j + 4 + i);
-                v |= (lo | (hi << 4)) << (8 * i);
-            }
-            w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
+
+    const int64_t rt = (int64_t)blockIdx.x / quads, gq = (int64_t)blockIdx.x % quads;
+    const int64_t row0 = rt * kTileRows, blk0 = gq * kRepackChunks * kTileBlocks;
+    const bool staged = aligned16 && row0 + kTileRows <= n && blk0 + kRepackChunks * kTileBlocks <= nb;
+    if (staged) {  // uniform per workgroup
+        for (int i = threadIdx.x; i < kPieces; i += kRepackThreads) {
+            const int r = i / (kRowB / 16), j = i % (kRowB / 16);
+            tile[i] = reinterpret_cast<const uint4*>(gguf + ((row0 + r) * nb + blk0) * kBPB)[j];
         }
-        reinterpret_cast<uint4*>(chunk)[e] = make_uint4(w[0], w[1], w[2], w[3]);
-    } else {
-        uint32_t w[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) |
-                   ((uint32_t)qs[4 * j + 2] << 16) | ((uint32_t)qs[4 * j + 3] << 24);
-        uint4* c4 = reinterpret_cast<uint4*>(chunk) + 2 * e;
-        c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        __syncthreads();
     }
+    const int t = threadIdx.x;
+    const int c = t / kTileEntries, e = t % kTileEntries;
+    const int64_t grp = gq * kRepackChunks + c;
+    if (grp >= groups) return;
+    const int64_t row = row0 + (e & 15), blk = grp * kTileBlocks + (e >> 4);
+    uint8_t* chunk = chunks + (rt * groups + grp) * kChunk;
+    uint16_t scale = 0;
+    uint32_t w[kCB / 4];
+#pragma unroll
+    for (int j = 0; j < kCB / 4; ++j) w[j] = 0;
+    if (row < n && blk < nb) {
+        uint8_t b[kBPB];
+        if (staged) {
+            const uint8_t* src = t8 + (e & 15) * kRowB + (c * kTileBlocks + (e >> 4)) * kBPB;
+#pragma unroll
+            for (int i = 0; i < kBPB; ++i) b[i] = src[i];
+        } else {
+            const uint8_t* src = gguf + (row * nb + blk) * kBPB;
+#pragma unroll
+            for (int i = 0; i < kBPB; ++i) b[i] = src[i];
+        }
+        scale = (uint16_t)(b[0] | (b[1] << 8));
+        const uint8_t* qs = b + 2;
+        if constexpr (kQ4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t lo = q4_code(qs, 8 * j + i);
+                    const uint32_t hi = q4_code(qs, 8 * j + 4 + i);
+                    v |= (lo | (hi << 4)) << (8 * i);
+                }
+                w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) | ((uint32_t)qs[4 * j + 2] << 16) |
+                       ((uint32_t)qs[4 * j + 3] << 24);
+        }
+    }
+    reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = scale;
+    uint4* c4 = reinterpret_cast<uint4*>(chunk + e * kCB);
+    c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
 // Chunked weight -> f32 [n][k].  One thread per 8 consecutive elements of a row
@@ -304,16 +323,16 @@ inline unsigned grid_for(int64_t items, int per_block) {
 }  // namespace
 
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
-    const int64_t nblocks = w.n * w.nb;
-    if (nblocks <= 0) return hipSuccess;
-    const int aligned = ((uintptr_t)gguf % 16) == 0;
-    const dim3 grid(grid_for(nblocks, kTile));
+    if (w.n_tiles <= 0 || w.groups <= 0) return hipSuccess;
+    const int aligned = ((uintptr_t)gguf % 16) == 0 && w.nb % 8 == 0;
+    const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
+    const dim3 grid((unsigned)(w.n_tiles * quads));
     if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
-                           w.groups, aligned, w.chunks);
+        hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups,
+                           quads, aligned, w.chunks);
     else
-        hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kTile), 0, s, gguf, nblocks, w.nb,
-                           w.groups, aligned, w.chunks);
+        hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups,
+                           quads, aligned, w.chunks);
     return hipGetLastError();
 }
 
