@@ -313,10 +313,18 @@ def main(argv=None) -> int:
     down = bench_gemv(qmm, hipr, stream, args.steps, args.warmup, N=4096, K=11008, seed=0x5EED0002)
     log(f"q4_0 gemv 4096x11008: wall {down['gbs_wall']:.1f} GB/s, kernel {down['gbs_kernel']:.1f} GB/s")
     gemm = None
+    prefill = []
     if not args.no_gemm:
         gemm = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
         log(f"q8_0 gemm M=512: wall {gemm['tflops_wall']:.1f} TFLOP/s, kernel "
             f"{gemm['tflops_kernel']:.1f} TFLOP/s")
+        # the other prefill sizes of BASELINE configs[3]
+        for m in (128, 2048):
+            r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 8), max(3, args.warmup // 4), M=m)
+            prefill.append({"workload": f"q8_0_gemm_n11008_k4096_m{m}_bf16x", "unit": "TFLOP/s",
+                            "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4)})
+            log(f"q8_0 gemm M={m}: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
     layer = None
     if not args.no_layer:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
@@ -382,6 +390,8 @@ def main(argv=None) -> int:
                          "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
                          "kernel_us": round(gemm["kernel_ms"] * 1e3, 3)},
         }
+    if prefill:
+        out["prefill_sizes"] = prefill
     if batched:
         out["batched_decode"] = batched
     if layer:
