@@ -203,8 +203,37 @@ def cpu_baseline(gemv: dict, seconds: float) -> dict:
             el_f = time.perf_counter() - t0
             if el_f >= seconds / 2:
                 break
+
+        # the same f32 GEMV on all cores, rows split evenly (OpenMP-style)
+        ya = np.empty((1, N), dtype=np.float32)
+
+        def part_asrun(i):
+            ya[:, rows[i]:rows[i + 1]] = oracle.cpu_asrun_linear(w[rows[i]:rows[i + 1]], x, None, False)
+
+        list(ex.map(part_asrun, range(threads)))
+        reps_a, t0 = 0, time.perf_counter()
+        while True:
+            list(ex.map(part_asrun, range(threads)))
+            reps_a += 1
+            el_a = time.perf_counter() - t0
+            if el_a >= seconds / 4:
+                break
     assert np.max(np.abs(y - y_ref)) <= 1e-3 * np.max(np.abs(y_ref))
     per_call_f = el_f / reps_f
+    assert np.array_equal(ya.view(np.uint32), y_ref.view(np.uint32))  # same per-row order
+    per_call_a = el_a / reps_a
+    # as written: every linear() call also materialises W^T (model.rs:1052), one thread
+    wt = np.empty(N * K, dtype=np.float32)
+    reps_t, t0 = 0, time.perf_counter()
+    while True:
+        yt = oracle.cpu_asrun_linear(w, x, wt, True)
+        reps_t += 1
+        el_t = time.perf_counter() - t0
+        if el_t >= seconds / 4:
+            break
+    assert np.max(np.abs(yt - y_ref)) <= 1e-3 * np.max(np.abs(y_ref))
+    per_call_t = el_t / reps_t
+    del wt
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -224,6 +253,14 @@ def cpu_baseline(gemv: dict, seconds: float) -> dict:
                             "cores": threads, "ms_per_call": round(per_call_f * 1e3, 3),
                             "sample": f"{reps_f} calls, quant_simd-style dequant+dot from the "
                                       f"Q4_0 blocks, {threads} threads"},
+        "all_cores_asrun": {"value": round(b / per_call_a / 1e9, 3), "unit": "GB/s",
+                            "cores": threads, "ms_per_call": round(per_call_a * 1e3, 3),
+                            "sample": f"{reps_a} calls, the f32 GEMV above with rows split over "
+                                      f"{threads} threads"},
+        "as_written": {"value": round(b / per_call_t / 1e9, 3), "unit": "GB/s", "cores": 1,
+                       "ms_per_call": round(per_call_t * 1e3, 3),
+                       "sample": f"{reps_t} calls, each also materialising W^T (model.rs:1052 "
+                                 f"weight.t().to_owned()) before the f32 product"},
     }
 
 
