@@ -140,8 +140,65 @@ struct Cursor {
             return false;
         }
         if (!need((size_t)len, "string data")) return false;
+        size_t valid_up_to = 0;
+        int error_len = 0;
+        if (!utf8_valid(p + off, (size_t)len, &valid_up_to, &error_len)) {
+            // String::from_utf8 -> "Invalid UTF-8 string: {Utf8Error}" (gguf.rs:1780)
+            char b[160];
+            if (error_len > 0)
+                snprintf(b, sizeof(b), "Invalid UTF-8 string: invalid utf-8 sequence of %d bytes from index %zu",
+                         error_len, valid_up_to);
+            else
+                snprintf(b, sizeof(b), "Invalid UTF-8 string: incomplete utf-8 byte sequence from index %zu",
+                         valid_up_to);
+            err = b;
+            return false;
+        }
         s->assign(reinterpret_cast<const char*>(p + off), (size_t)len);
         off += (size_t)len;
+        return true;
+    }
+    // UTF-8 well-formedness as String::from_utf8 checks it (RFC 3629: no overlong
+    // forms, no surrogates, nothing above U+10FFFF).  On failure: the index of the
+    // first bad sequence and the number of bytes that make it invalid (1-3), or 0
+    // when the input ends inside a sequence.
+    static bool utf8_valid(const uint8_t* s, size_t n, size_t* valid_up_to, int* error_len) {
+        size_t i = 0;
+        auto cont = [&](size_t j) { return (s[j] & 0xC0) == 0x80; };
+        auto fail = [&](int len) {
+            *valid_up_to = i;
+            *error_len = len;
+            return false;
+        };
+        while (i < n) {
+            const uint8_t b = s[i];
+            if (b < 0x80) {
+                ++i;
+                continue;
+            }
+            int width = 0;
+            uint8_t lo = 0x80, hi = 0xBF;  // allowed range of the second byte
+            if (b >= 0xC2 && b <= 0xDF) {
+                width = 2;
+            } else if (b >= 0xE0 && b <= 0xEF) {
+                width = 3;
+                if (b == 0xE0) lo = 0xA0;
+                if (b == 0xED) hi = 0x9F;
+            } else if (b >= 0xF0 && b <= 0xF4) {
+                width = 4;
+                if (b == 0xF0) lo = 0x90;
+                if (b == 0xF4) hi = 0x8F;
+            } else {
+                return fail(1);
+            }
+            if (i + 1 >= n) return fail(0);
+            if (s[i + 1] < lo || s[i + 1] > hi) return fail(1);
+            for (int j = 2; j < width; ++j) {
+                if (i + j >= n) return fail(0);
+                if (!cont(i + j)) return fail(j);
+            }
+            i += (size_t)width;
+        }
         return true;
     }
     bool type_id(bool one_byte, uint32_t* t, const char* what) {

@@ -173,3 +173,103 @@ def test_loader_names_and_shapes(tmp_path):
     t = g.tensors["model.layers.0.ffn.up_proj"]
     assert t.dims == [K, N] and t.data_size() == q.size
     assert np.array_equal(g.get_tensor_data(t.name), q)
+
+
+def _utf8_expectation(raw: bytes) -> str:
+    """The reference's message for a string of these bytes (gguf.rs:1780,
+    String::from_utf8), pinned by Python's strict UTF-8 decoder: the same RFC 3629
+    rules and the same error position and length (maximal invalid subpart)."""
+    try:
+        raw.decode("utf-8")
+        return ""
+    except UnicodeDecodeError as e:
+        if e.reason == "unexpected end of data":
+            return f"Invalid UTF-8 string: incomplete utf-8 byte sequence from index {e.start}"
+        return f"Invalid UTF-8 string: invalid utf-8 sequence of {e.end - e.start} bytes from index {e.start}"
+
+
+UTF8_CASES = [
+    b"ab\xffcd",               # invalid start byte
+    b"ab\xc0\x80cd",           # overlong NUL
+    b"ab\xe0\x80\x80cd",       # overlong 3-byte form
+    b"ab\xed\xa0\x80cd",       # UTF-16 surrogate
+    b"ab\xf4\x90\x80\x80cd",   # above U+10FFFF
+    b"ab\xe4\xb8xcd",          # third byte not a continuation
+    b"ab\xf0\x9f\x98xcd",      # fourth byte not a continuation
+    b"ab\xe4\xb8",             # ends inside a sequence
+    "权重.中文".encode(),       # valid multi-byte text
+    "w\U0001F642".encode(),    # valid 4-byte sequence
+]
+
+
+@pytest.mark.parametrize("dialect", [G.REFERENCE, G.STANDARD])
+@pytest.mark.parametrize("where", ["key", "value", "tensor"])
+@pytest.mark.parametrize("raw", UTF8_CASES)
+def test_strings_must_be_utf8(tmp_path, dialect, where, raw):
+    """Every GGUF string (keys, string values, tensor names) goes through
+    String::from_utf8 in the reference: invalid UTF-8 is an error naming the position,
+    valid text is kept byte for byte."""
+    hole = "Q" * len(raw)
+    key, value, tname = (hole if where == "key" else "k"), (hole if where == "value" else "v"), \
+        (hole if where == "tensor" else "t")
+    data = fx.build([(key, fx.STRING, value)], [(tname, [32], 0, bytes(128))],
+                    "reference" if dialect == G.REFERENCE else "standard")
+    assert data.count(hole.encode()) == 1
+    data = data.replace(hole.encode(), raw)
+    want = _utf8_expectation(raw)
+    if want:
+        with pytest.raises(G.GgufError) as ei:
+            G.GgufFile(write(tmp_path, data), dialect)
+        assert want in str(ei.value)
+        return
+    g = G.GgufFile(write(tmp_path, data), dialect)
+    text = raw.decode()
+    if where == "key":
+        assert g.keys == [text] and g.get_string(text) == "v"
+    elif where == "value":
+        assert g.get_string("k") == text
+    else:
+        assert list(g.tensors) == [text] and g.get_tensor_data(text) is not None
+
+
+def test_random_mutations_parse_or_fail_cleanly(tmp_path):
+    """Fixed-seed mutation fuzzing of a multi-tensor file in both dialects: byte
+    overwrites, 64-bit counts / lengths / offsets set to extreme values, truncation.
+    Every file either parses (and its tensor views stay in the file) or raises
+    GgufError; nothing else escapes and nothing crashes."""
+    import random
+    rng = random.Random(20261202)
+    q = np.random.default_rng(1).integers(0, 256, 2 * 18 * 4, dtype=np.uint8)
+    meta = [("general.architecture", fx.STRING, "llama"), ("a", fx.ARRAY, (fx.U32, [1, 2])), ("f", fx.F32, 1.5)]
+    tens = [("w", [64, 4], 2, q.tobytes()), ("x", [8], 0, bytes(32))]
+    bases = {G.REFERENCE: fx.build(meta, tens, "reference"), G.STANDARD: fx.build(meta, tens, "standard")}
+    path = write(tmp_path, b"")
+    parsed = failed = 0
+    for _ in range(600):
+        dialect = rng.choice(sorted(bases))
+        b = bytearray(bases[dialect])
+        for _ in range(rng.randint(1, 6)):
+            pos = rng.randrange(len(b))
+            r = rng.random()
+            if r < 0.5:
+                b[pos] = rng.randrange(256)
+            elif r < 0.85 and pos + 8 <= len(b):
+                b[pos:pos + 8] = struct.pack("<Q", rng.choice([0, 1, 2**31, 2**32 - 1, 2**63, 2**64 - 1,
+                                                                rng.randrange(2**64)]))
+            else:
+                del b[pos:]
+                break
+        with open(path, "wb") as f:
+            f.write(bytes(b))
+        try:
+            g = G.GgufFile(path, dialect)
+        except G.GgufError:
+            failed += 1
+            continue
+        parsed += 1
+        for name in g.tensors:
+            view = g.get_tensor_data(name)
+            if view is not None:  # inside the file, and every byte readable
+                assert len(view) <= len(b)
+                int(view.sum(dtype=np.uint64))
+    assert parsed > 0 and failed > 0
