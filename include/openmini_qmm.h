@@ -114,11 +114,13 @@ int openmini_qmm_device_info(char* buf, size_t buf_len);
 
 /* GgufTensor::data_size (src/model/inference/gguf.rs:431-438):
  * ceil(n_elements / block_size) * bytes_per_block for every type id above.  Pure host
- * computation. */
+ * computation.  n_elements above 2^48 -> INVALID_PARAM (every entry point taking an
+ * element count has this limit, so no size computed from one wraps around). */
 int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes);
 
 /* GpuQuantOps::estimate_memory_usage (quant_simd.rs:2985): device bytes a
- * dequantization of n_elements needs (GGUF input + f32 output). */
+ * dequantization of n_elements needs (GGUF input + f32 output); SIZE_MAX above 2^48
+ * elements. */
 size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
 
 /* ---- weight upload / repack (the loader's layout step) ---------------------------

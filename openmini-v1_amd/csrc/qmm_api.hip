@@ -70,9 +70,19 @@ bool type_supported(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPEN
 // quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
 bool safe_type(int type) { return type_supported(type) || type == OPENMINI_QMM_Q4_1; }
 // ceil(n / block_size) * bytes_per_block (gguf.rs:431-438); 0 for unknown types.
+// Element counts above 2^48 (1 PB of f32) are rejected, so every size computed
+// from one (bytes of any layout, n * sizeof(float)) fits in 64 bits.
+constexpr size_t kMaxElements = (size_t)1 << 48;
+
 size_t layout_bytes(int type, size_t n) {
     const int bs = qmm::layout_block_size(type);
     return bs ? (n + bs - 1) / bs * (size_t)qmm::layout_bytes_per_block(type) : 0;
+}
+
+int check_elements(size_t n) {
+    if (n > kMaxElements)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "n_elements=%zu exceeds the maximum 2^48", n);
+    return OPENMINI_QMM_OK;
 }
 
 // Device probing is done once per device; the result is cached.
@@ -283,11 +293,14 @@ int openmini_qmm_device_info(char* buf, size_t buf_len) {
 int openmini_qmm_required_bytes(int type, size_t n_elements, size_t* out_bytes) {
     if (!out_bytes) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_bytes");
     if (!qmm::layout_block_size(type)) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d", type);
+    const int rc = check_elements(n_elements);
+    if (rc != OPENMINI_QMM_OK) return rc;
     *out_bytes = layout_bytes(type, n_elements);
     return ok();
 }
 
 size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements) {
+    if (n_elements > kMaxElements) return SIZE_MAX;
     const size_t in = qmm::layout_block_size(type) ? layout_bytes(type, n_elements) : n_elements * sizeof(float);
     return in + n_elements * sizeof(float);
 }
@@ -483,6 +496,8 @@ static int validate_dequant(int type, size_t gguf_bytes, size_t n, size_t* expec
     if (expected_bytes) *expected_bytes = 0;
     if (!safe_type(type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "UnsupportedType(%d)", type);
+    const int rc = check_elements(n);
+    if (rc != OPENMINI_QMM_OK) return rc;
     const size_t need = layout_bytes(type, n);
     if (gguf_bytes < need) {
         if (expected_bytes) *expected_bytes = need;
@@ -537,9 +552,11 @@ int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf
                                        void* stream) {
     if (!qmm::layout_block_size(type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "tensor type %d is not implemented", type);
+    int rc = check_elements(n);
+    if (rc != OPENMINI_QMM_OK) return rc;
     if (n == 0) return ok();
     if (!d_out || (!d_gguf && gguf_bytes)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
-    int rc = ensure_device(nullptr);
+    rc = ensure_device(nullptr);
     if (rc != OPENMINI_QMM_OK) return rc;
     const size_t used = std::min(gguf_bytes, layout_bytes(type, n));
     hipError_t e = qmm::launch_dequant_layout(type, static_cast<const uint8_t*>(d_gguf), used, n, d_out,
@@ -551,9 +568,11 @@ int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf
 int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out) {
     if (!qmm::layout_block_size(type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "tensor type %d is not implemented", type);
+    int rc = check_elements(n);
+    if (rc != OPENMINI_QMM_OK) return rc;
     if (n == 0) return ok();
     if (!out || (!gguf && gguf_bytes)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
-    int rc = ensure_device(nullptr);
+    rc = ensure_device(nullptr);
     if (rc != OPENMINI_QMM_OK) return rc;
     const size_t used = std::min(gguf_bytes, layout_bytes(type, n));
     void *din = nullptr, *dout = nullptr;

@@ -21,8 +21,8 @@
 // Every read is bounds-checked against the mapping: a malformed file is an error
 // (status + message), never a crash.  The reference's messages are kept where it has
 // them ("File too small", "Invalid GGUF magic number", "Unexpected EOF", "String too
-// long", "Unknown value type", "Too many dimensions", "Unknown tensor type", "Tensor
-// data out of bounds", "Tensor not found").
+// long", "Invalid UTF-8 string", "Unknown value type", "Too many dimensions", "Unknown
+// tensor type", "Tensor data out of bounds", "Tensor not found").
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -344,16 +344,25 @@ bool parse(openmini_qmm_gguf& g, bool reference_dialect, std::string* err) {
     return true;
 }
 
+// Element count, saturating: UINT64_MAX when the product of the dims overflows.
 uint64_t elements_of(const Tensor& t) {
     uint64_t n = 1;
-    for (uint64_t d : t.dims) n *= d;
+    for (uint64_t d : t.dims) {
+        if (d != 0 && n > UINT64_MAX / d) return UINT64_MAX;
+        n *= d;
+    }
     return n;
 }
 
+// Data bytes (GgufTensor::data_size, gguf.rs:431-438).  Tensors of more than 2^48
+// elements get UINT64_MAX, which no file holds, so they report "Tensor data out of
+// bounds" instead of a size that wrapped around.
 uint64_t data_size_of(const Tensor& t) {
     uint64_t bs = 0, bpb = 0;
     type_geometry(t.type, &bs, &bpb);
-    return (elements_of(t) + bs - 1) / bs * bpb;
+    const uint64_t n = elements_of(t);
+    if (n > ((uint64_t)1 << 48)) return UINT64_MAX;
+    return (n + bs - 1) / bs * bpb;
 }
 
 bool fits(const openmini_qmm_gguf& g, const Tensor& t) {

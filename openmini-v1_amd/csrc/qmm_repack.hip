@@ -363,6 +363,23 @@ hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, fl
 
 hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, size_t n_elems, float* out,
                                  hipStream_t s) {
+    // A launch covers fewer than 2^32 work-items: larger tensors go in slices of 2^30
+    // elements (a whole number of blocks of every layout), each reading its own
+    // blocks and writing its own outputs.
+    constexpr size_t kSlice = (size_t)1 << 30;
+    if (n_elems > kSlice) {
+        const int bs = layout_block_size(type);
+        const int bpb = layout_bytes_per_block(type);
+        if (bs <= 0 || kSlice % (size_t)bs != 0) return hipErrorInvalidValue;
+        for (size_t e0 = 0; e0 < n_elems; e0 += kSlice) {
+            const size_t n = n_elems - e0 < kSlice ? n_elems - e0 : kSlice;
+            const size_t skip = e0 / (size_t)bs * (size_t)bpb;  // bytes before this slice
+            const size_t avail = bytes > skip ? bytes - skip : 0;
+            const hipError_t e = launch_dequant_layout(type, avail ? gguf + skip : gguf, avail, n, out + e0, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     if (n_elems == 0) return hipSuccess;
     if (type == OPENMINI_QMM_F32 || type == OPENMINI_QMM_F16) {
         const size_t esz = type == OPENMINI_QMM_F16 ? 2 : 4;

@@ -123,3 +123,30 @@ def test_log_callback_receives_every_failure():
     assert "multiple of 32" in seen[1][1]
     assert L.openmini_qmm_required_bytes(16, 32, ctypes.byref(out)) == _native.ERR_UNSUPPORTED
     assert len(seen) == 2  # logging is off again
+
+
+def test_element_counts_are_bounded():
+    """Element counts above 2^48 are rejected before any size is computed from them (no
+    wrapped byte count can pass the InsufficientData check), on every entry point that
+    takes one; the byte count at the limit is the closed form ceil(n / bs) * bpb."""
+    from openmini_qmm import _native
+    L = _native.lib()
+    out = ctypes.c_size_t()
+    lim = 1 << 48
+    for t, bs, bpb in ((0, 1, 4), (1, 1, 2), (2, 32, 18), (3, 32, 20), (7, 32, 34), (10, 256, 68),
+                       (11, 256, 162), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 258)):
+        assert L.openmini_qmm_required_bytes(t, lim, ctypes.byref(out)) == 0
+        assert out.value == -(-lim // bs) * bpb
+        for n in (lim + 1, 2**62 + 1, 2**64 - 1):
+            assert L.openmini_qmm_required_bytes(t, n, ctypes.byref(out)) == _native.ERR_INVALID_PARAM
+            assert b"exceeds the maximum 2^48" in L.openmini_qmm_last_error()
+            assert L.openmini_qmm_estimate_memory_usage(t, n) == 2**64 - 1
+    buf = (ctypes.c_uint8 * 16)()
+    dst = (ctypes.c_float * 4)()
+    exp = ctypes.c_size_t()
+    # F32 with 2^62 + 1 elements: 4 n wraps to 4 bytes, which the 16-byte buffer would cover
+    assert L.openmini_qmm_dequantize_any(0, buf, 16, 2**62 + 1, dst) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_dequantize_any_device(0, buf, 16, 2**62 + 1, dst, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_dequantize(2, buf, 16, 2**62 + 1, dst, ctypes.byref(exp)) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_dequantize_device(2, buf, 16, 2**62 + 1, dst, None, ctypes.byref(exp)) == \
+        _native.ERR_INVALID_PARAM

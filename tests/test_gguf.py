@@ -273,3 +273,13 @@ def test_random_mutations_parse_or_fail_cleanly(tmp_path):
                 assert len(view) <= len(b)
                 int(view.sum(dtype=np.uint64))
     assert parsed > 0 and failed > 0
+
+
+@pytest.mark.parametrize("dims", [[2**33, 2**33], [3, 2**62 + 1], [2**40, 2**9]])
+def test_oversized_tensor_dims_are_out_of_bounds(tmp_path, dims):
+    """A tensor whose element count overflows 64 bits, wraps to a small byte count
+    (F32: 4 * (3 * (2^62 + 1)) mod 2^64 = 12), or exceeds 2^48 elements reports
+    "Tensor data out of bounds" instead of a wrapped size: no view, no dequantization."""
+    data = fx.build([], [("t", dims, 0, bytes(64))], "reference")
+    g = G.GgufFile(write(tmp_path, data), G.REFERENCE)
+    assert g.get_tensor_data("t") is None

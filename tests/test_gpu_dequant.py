@@ -235,3 +235,44 @@ def test_gpu_quant_ops_mirror(qmm, orc):
     assert np.all(outs[1][512:] == 0.0) and np.all(np.signbit(outs[2]))
     with pytest.raises(ops.GpuQuantOpsError):
         ops.batch_dequantize_gpu([(16, bytes(64), 256)])
+
+
+@pytest.mark.parametrize("qtype", [2, 12, 1])
+def test_dequant_beyond_one_launch_slice(qmm, orc, qtype):
+    """Tensors above 2^30 elements are dequantized in slices of 2^30 (a launch stays below
+    2^32 work-items).  Around the slice boundary and at the tail the output matches the
+    oracle bit for bit; with a buffer that ends inside the second slice, everything
+    after the last whole block is 0.0 and everything before it is unchanged."""
+    import ctypes
+    from openmini_qmm import _native
+    L = _native.lib()
+    bs, bpb = LAYOUTS[qtype]
+    S = 1 << 30
+    nblk = S // bs + 4096
+    n = nblk * bs
+    print(f"dequantize_any_device type={qtype} n={n}", flush=True)
+    raw = np.zeros(nblk * bpb, dtype=np.uint8)
+    b0 = S // bs - 64  # 128 random blocks straddling the boundary, 64 at the end
+    raw[b0 * bpb:(b0 + 128) * bpb] = layout_bytes(qtype, 128, seed=qtype + 900)
+    raw[(nblk - 64) * bpb:] = layout_bytes(qtype, 64, seed=qtype + 901)
+    d_in = qmm.DeviceBuffer.from_numpy(raw)
+    d_out = qmm.DeviceBuffer(n * 4)
+
+    def window(e0, count):
+        host = np.empty(count, dtype=np.float32)
+        src = ctypes.c_void_p(d_out.ptr.value + 4 * e0)
+        assert L.openmini_qmm_memcpy_d2h(host.ctypes.data_as(ctypes.c_void_p), src, host.nbytes, None) == 0
+        return host
+
+    for nbytes in (raw.size, (S // bs + 10) * bpb + bpb // 2):
+        d_out.fill(0xFF)  # NaN pattern: every output must be written
+        assert L.openmini_qmm_dequantize_any_device(qtype, d_in.ptr, nbytes, n, d_out.ptr, None) == 0
+        ref = orc.dequantize(qtype, raw[b0 * bpb:(b0 + 128) * bpb][: max(0, nbytes - b0 * bpb)], 128 * bs)
+        assert np.array_equal(bits(window(b0 * bs, 128 * bs)), bits(ref)), nbytes
+        tail = window(n - 64 * bs, 64 * bs)
+        if nbytes == raw.size:
+            assert np.array_equal(bits(tail), bits(orc.dequantize(qtype, raw[(nblk - 64) * bpb:], 64 * bs)))
+        else:
+            assert np.all(tail == 0.0) and not np.any(np.signbit(tail))
+    d_in.free()
+    d_out.free()
