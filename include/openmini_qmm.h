@@ -224,6 +224,23 @@ int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf
 /* Same on host memory, synchronous. */
 int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, size_t n, float* out);
 
+/* quant_simd::convert_to_soa_layout (src/model/inference/quant_simd.rs:3245-3397), the
+ * reference's AoS -> SoA byte permutation:
+ *   - empty input or n == 0: 0 bytes;
+ *   - F32 / F16: the first min(n * 4 | 2, len) bytes, copied;
+ *   - Q4_0 / Q8_0: [the fp16 scale of each of ceil(n / 32) blocks][byte position 0 of
+ *     every block] ... [the last position]; Q4_1: [scales][mins][16 positions]; a
+ *     field is copied only when both its bytes are in the input, missing code bytes
+ *     are 0;
+ *   - any other GgufTensorType id: the input, copied.
+ * soa_bytes gives the output length (UNSUPPORTED for ids GgufTensorType does not have;
+ * n above 2^48 -> INVALID_PARAM).  The device call runs on `stream`; the host call is
+ * synchronous.  The reference's unused `_block_size` argument is dropped. */
+int openmini_qmm_soa_bytes(int type, size_t len, size_t n, size_t* out_bytes);
+int openmini_qmm_convert_to_soa_device(int type, const void* d_data, size_t len, size_t n,
+                                       void* d_out, void* stream);
+int openmini_qmm_convert_to_soa(int type, const void* data, size_t len, size_t n, void* out);
+
 /* ---- GGUF files: the loader's raw-block path ----------------------------------------
  * GgufFile (src/model/inference/gguf.rs:1357-2110) and QuantizedWeightLoader
  * (quant_loader.rs:54-138) without dequantize-at-load.  The file is memory-mapped once;

@@ -593,6 +593,60 @@ int openmini_qmm_dequantize_any(int type, const void* gguf, size_t gguf_bytes, s
     return ok();
 }
 
+// GgufTensorType ids (gguf.rs:219-276): 0..29 except 6 and 9.
+static bool gguf_type_id(int t) { return t >= 0 && t <= 29 && t != 6 && t != 9; }
+
+int openmini_qmm_soa_bytes(int type, size_t len, size_t n, size_t* out_bytes) {
+    if (!out_bytes) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_bytes");
+    *out_bytes = 0;
+    if (!gguf_type_id(type)) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unknown tensor type %d", type);
+    const int rc = check_elements(n);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    *out_bytes = qmm::soa_bytes(type, len, n);
+    return ok();
+}
+
+int openmini_qmm_convert_to_soa_device(int type, const void* d_data, size_t len, size_t n, void* d_out,
+                                       void* stream) {
+    size_t total = 0;
+    int rc = openmini_qmm_soa_bytes(type, len, n, &total);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (total == 0) return ok();
+    if (!d_data || !d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipError_t e = qmm::launch_convert_to_soa(type, static_cast<const uint8_t*>(d_data), len, n,
+                                              static_cast<uint8_t*>(d_out), as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "convert_to_soa launch");
+    return ok();
+}
+
+int openmini_qmm_convert_to_soa(int type, const void* data, size_t len, size_t n, void* out) {
+    size_t total = 0;
+    int rc = openmini_qmm_soa_bytes(type, len, n, &total);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (total == 0) return ok();
+    if (!data || !out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    void *din = nullptr, *dout = nullptr;
+    hipError_t e = hipMalloc(&din, len);
+    if (e == hipSuccess) e = hipMalloc(&dout, total);
+    if (e != hipSuccess) {
+        (void)hipFree(din);
+        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for convert_to_soa failed: %s", hipGetErrorString(e));
+    }
+    e = hipMemcpy(din, data, len, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = qmm::launch_convert_to_soa(type, static_cast<const uint8_t*>(din), len, n, static_cast<uint8_t*>(dout),
+                                       nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dout, total, hipMemcpyDeviceToHost);
+    (void)hipFree(din);
+    (void)hipFree(dout);
+    if (e != hipSuccess) return hip_fail(e, "convert_to_soa");
+    return ok();
+}
+
 int openmini_qmm_malloc(void** d_ptr, size_t bytes) {
     if (!d_ptr) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null d_ptr");
     *d_ptr = nullptr;

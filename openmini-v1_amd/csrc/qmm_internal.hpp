@@ -161,6 +161,11 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
                             bool gate_in_y = false);
 
+// quant_simd::convert_to_soa_layout: output bytes, and the conversion of `len` device
+// bytes (n elements) into `out` on stream s.
+size_t soa_bytes(int type, size_t len, size_t n);
+hipError_t launch_convert_to_soa(int type, const uint8_t* src, size_t len, size_t n, uint8_t* out, hipStream_t s);
+
 // quant::dequantize semantics for every layout the library knows (F32, F16, Q4_0,
 // Q4_1, Q8_0, Q2_K..Q8_K): complete blocks of `bytes` are dequantized, the rest of the
 // n_elems outputs are zero.  hipErrorInvalidValue for other types.

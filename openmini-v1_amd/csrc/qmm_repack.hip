@@ -316,6 +316,29 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restric
         dst[i] = src[i];
 }
 
+// quant_simd::convert_to_soa_layout's block arms (quant_simd.rs:3300-3397): output byte
+// o is byte (o & 1) of fp16 field f (scale; Q4_1 also min) of block b for o below
+// 2 * fields * blocks, else code position pos of block b, position-major.  A field is
+// copied only when both of its bytes are in the input; missing code bytes are 0.
+__global__ __launch_bounds__(256) void soa_kernel(const uint8_t* __restrict__ src, size_t len, size_t blocks,
+                                                  int bpb, int fields, uint8_t* __restrict__ out, size_t total) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t hdr = 2 * (size_t)fields * blocks;
+    for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
+        uint8_t v;
+        if (o < hdr) {
+            const size_t f = o / (2 * blocks), r = o % (2 * blocks);
+            const size_t off = (r >> 1) * bpb + 2 * f;
+            v = off + 2 <= len ? src[off + (r & 1)] : 0;
+        } else {
+            const size_t q = o - hdr, pos = q / blocks, b = q % blocks;
+            const size_t off = b * bpb + 2 * (size_t)fields + pos;
+            v = off < len ? src[off] : 0;
+        }
+        out[o] = v;
+    }
+}
+
 inline unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)((items + per_block - 1) / per_block);
 }
@@ -358,6 +381,27 @@ hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, fl
         hipLaunchKernelGGL(dequant_gguf_kernel<18>, grid, dim3(256), 0, s, gguf, n_elems, out);
     else
         hipLaunchKernelGGL(dequant_gguf_kernel<34>, grid, dim3(256), 0, s, gguf, n_elems, out);
+    return hipGetLastError();
+}
+
+size_t soa_bytes(int type, size_t len, size_t n) {
+    if (len == 0 || n == 0) return 0;
+    if (type == OPENMINI_QMM_F32) return n * 4 < len ? n * 4 : len;
+    if (type == OPENMINI_QMM_F16) return n * 2 < len ? n * 2 : len;
+    if (type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_1 || type == OPENMINI_QMM_Q8_0)
+        return (n + kQK - 1) / kQK * (size_t)layout_bytes_per_block(type);
+    return len;
+}
+
+hipError_t launch_convert_to_soa(int type, const uint8_t* src, size_t len, size_t n, uint8_t* out, hipStream_t s) {
+    const size_t total = soa_bytes(type, len, n);
+    if (total == 0) return hipSuccess;
+    if (type != OPENMINI_QMM_Q4_0 && type != OPENMINI_QMM_Q4_1 && type != OPENMINI_QMM_Q8_0)
+        return hipMemcpyAsync(out, src, total, hipMemcpyDeviceToDevice, s);  // the copy arms
+    const size_t blocks = (n + kQK - 1) / kQK;
+    const int64_t wgs = ((int64_t)(total / 256) + 1) < 65536 ? (int64_t)(total / 256) + 1 : 65536;
+    hipLaunchKernelGGL(soa_kernel, dim3((unsigned)wgs), dim3(256), 0, s, src, len, blocks, layout_bytes_per_block(type),
+                       type == OPENMINI_QMM_Q4_1 ? 2 : 1, out, total);
     return hipGetLastError();
 }
 

@@ -9,6 +9,7 @@ from .layer import (AttentionWeights, FFNWeights, ffn_gate_up, ffn_gate_up_bf16,
                     gemv_multi)
 from .ops import (DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,  # noqa: F401
                   InsufficientData, InvalidInput, QuantError, QuantizedWeight, Stream,
-                  UnsupportedType, dequantize, dequantize_simd, get_gemm_engine, init, linear,
+                  UnsupportedType, convert_to_soa_layout, dequantize, dequantize_simd,
+                  get_gemm_engine, init, linear,
                   linear_gemm, safe_dequantize, safe_dequantize_q4_0, safe_dequantize_q4_1,
                   safe_dequantize_q8_0, stream_copy)

@@ -265,6 +265,25 @@ def safe_dequantize_q4_1(data, n: int) -> np.ndarray:
     return safe_dequantize(data, GgufTensorType.Q4_1, n)
 
 
+def convert_to_soa_layout(data, tensor_type, n: int, block_size: int = 32) -> np.ndarray:
+    """quant_simd::convert_to_soa_layout (quant_simd.rs:3245-3397) on the GPU: the AoS ->
+    SoA byte permutation of Q4_0 / Q4_1 / Q8_0 blocks, the truncated copy of F32 / F16,
+    the input itself for other types; empty for empty input or n == 0.  block_size is
+    unused, as in the reference."""
+    del block_size
+    tt = int(tensor_type)
+    buf = _as_u8(data)
+    total = ctypes.c_size_t(0)
+    rc = lib().openmini_qmm_soa_bytes(tt, buf.size, int(n), ctypes.byref(total))
+    if rc == _native.ERR_UNSUPPORTED:
+        raise UnsupportedType(tensor_type)
+    check(rc)
+    out = np.empty(total.value, dtype=np.uint8)
+    if total.value:
+        check(lib().openmini_qmm_convert_to_soa(tt, _ptr(buf), buf.size, int(n), _ptr(out)))
+    return out
+
+
 # ---- GpuQuantOps ----------------------------------------------------------------------
 
 class HipQuantOps:

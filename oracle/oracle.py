@@ -53,6 +53,7 @@ def lib():
             "orc_dequantize": (i, [i, p, sz, sz, p]),
             "orc_safe_dequantize": (i, [i, p, sz, sz, p, ctypes.POINTER(sz)]),
             "orc_convert_to_soa": (sz, [i, p, sz, sz, p]),
+            "orc_soa_bytes": (sz, [i, sz, sz]),
             "orc_quantize_q4_0": (None, [p, sz, p]),
             "orc_quantize_q8_0": (None, [p, sz, p]),
             "orc_linear_f64": (None, [i, p, sz, sz, p, sz, p]),
@@ -129,10 +130,12 @@ def restated(qtype: int) -> bool:
 
 
 def convert_to_soa(qtype: int, data, n: int) -> np.ndarray:
+    """quant_simd::convert_to_soa_layout (quant_simd.rs:3245-3397), every arm."""
     d = _u8(data)
-    blocks = (n + QK - 1) // QK
-    out = np.zeros(max(blocks * BYTES_PER_BLOCK.get(qtype, 1), 1), dtype=np.uint8)
+    total = lib().orc_soa_bytes(qtype, d.size, n)
+    out = np.zeros(max(total, 1), dtype=np.uint8)
     m = lib().orc_convert_to_soa(qtype, _ptr(d) if d.size else None, d.size, n, _ptr(out))
+    assert m == total
     return out[:m]
 
 

@@ -18,7 +18,8 @@
  *                           2093-2130, quant_simd.rs:4270-4290), hand-computed blocks
  *                           for every field of each layout, and a numpy restatement
  *   orc_safe_dequantize     InsufficientData payloads of the regression tests
- *   orc_convert_to_soa      quant_simd.rs KATs (lengths 72/68, first scale bytes)
+ *   orc_convert_to_soa      quant_simd.rs KATs (lengths 72/68/60, first scale bytes,
+ *                           empty input)
  *                           plus a brute-force permutation check
  *   orc_quantize_*          not in the reference (synthetic-weight generator fixed by
  *                           BASELINE configs = ggml's textbook quantizers): pinned by
@@ -427,26 +428,47 @@ int orc_safe_dequantize(int type, const uint8_t *data, size_t len, size_t n, flo
     return 0;
 }
 
-/* quant_simd::convert_to_soa_layout for Q4_0 / Q8_0, quant_simd.rs:3265-3293,
- * 3300-3327, 3370-3397: [all fp16 scales][byte position 0 of every block]...
- * [last position of every block]; bytes missing from `data` are 0.  Returns the
- * output length (blocks * bpb), 0 for empty input. */
-size_t orc_convert_to_soa(int type, const uint8_t *data, size_t len, size_t n, uint8_t *out) {
+/* quant_simd::convert_to_soa_layout (quant_simd.rs:3245-3293) and its arms
+ * convert_q4_0_to_soa (:3300-3327), convert_q4_1_to_soa (:3330-3367),
+ * convert_q8_0_to_soa (:3370-3397):
+ *   - empty data or n == 0: nothing;
+ *   - F32 / F16: the first min(n * 4 | 2, len) bytes, copied;
+ *   - Q4_0 / Q8_0: [fp16 scale of every block][byte position 0 of every block] ...
+ *     [last position of every block]; Q4_1: [scales][mins][16 positions]; for
+ *     ceil(n / 32) blocks, bytes missing from `data` read as 0;
+ *   - any other type: all of `data`, copied.
+ * Returns the output length. */
+size_t orc_soa_bytes(int type, size_t len, size_t n) {
     if (len == 0 || n == 0) return 0;
+    if (type == ORC_F32) return n * 4 < len ? n * 4 : len;
+    if (type == ORC_F16) return n * 2 < len ? n * 2 : len;
+    if (type == ORC_Q4_0 || type == ORC_Q4_1 || type == ORC_Q8_0)
+        return (n + QK - 1) / QK * orc_bytes_per_block(type);
+    return len;
+}
+
+size_t orc_convert_to_soa(int type, const uint8_t *data, size_t len, size_t n, uint8_t *out) {
+    size_t total = orc_soa_bytes(type, len, n);
+    if (type != ORC_Q4_0 && type != ORC_Q4_1 && type != ORC_Q8_0) {
+        memcpy(out, data, total);
+        return total;
+    }
+    if (total == 0) return 0;
     size_t bpb = orc_bytes_per_block(type);
-    if (type != ORC_Q4_0 && type != ORC_Q8_0) return 0;
-    size_t nq = bpb - 2;
+    size_t fields = type == ORC_Q4_1 ? 2 : 1; /* fp16 scale (and min) per block */
+    size_t nq = bpb - 2 * fields;
     size_t blocks = (n + QK - 1) / QK;
     size_t o = 0;
-    for (size_t b = 0; b < blocks; ++b) {
-        size_t off = b * bpb;
-        if (off + 2 <= len) { out[o] = data[off]; out[o + 1] = data[off + 1]; }
-        else { out[o] = 0; out[o + 1] = 0; }
-        o += 2;
-    }
+    for (size_t f = 0; f < fields; ++f)
+        for (size_t b = 0; b < blocks; ++b) {
+            size_t off = b * bpb + 2 * f;
+            if (off + 2 <= len) { out[o] = data[off]; out[o + 1] = data[off + 1]; }
+            else { out[o] = 0; out[o + 1] = 0; }
+            o += 2;
+        }
     for (size_t pos = 0; pos < nq; ++pos)
         for (size_t b = 0; b < blocks; ++b) {
-            size_t off = b * bpb + 2 + pos;
+            size_t off = b * bpb + 2 * fields + pos;
             out[o++] = off < len ? data[off] : 0;
         }
     return o;

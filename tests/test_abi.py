@@ -150,3 +150,19 @@ def test_element_counts_are_bounded():
     assert L.openmini_qmm_dequantize(2, buf, 16, 2**62 + 1, dst, ctypes.byref(exp)) == _native.ERR_INVALID_PARAM
     assert L.openmini_qmm_dequantize_device(2, buf, 16, 2**62 + 1, dst, None, ctypes.byref(exp)) == \
         _native.ERR_INVALID_PARAM
+
+
+def test_soa_bytes_host_rules(orc):
+    """openmini_qmm_soa_bytes: the output length of convert_to_soa_layout for every arm,
+    against the oracle's restatement; ids GgufTensorType lacks are UNSUPPORTED."""
+    from openmini_qmm import _native
+    L = _native.lib()
+    out = ctypes.c_size_t()
+    for t in list(range(0, 30)):
+        for length, n in ((0, 5), (37, 0), (37, 5), (1000, 33), (18 * 4, 128), (3, 1 << 40)):
+            rc = L.openmini_qmm_soa_bytes(t, length, n, ctypes.byref(out))
+            if t in (6, 9):
+                assert rc == _native.ERR_UNSUPPORTED
+                continue
+            assert rc == 0 and out.value == orc.lib().orc_soa_bytes(t, length, n), (t, length, n)
+    assert L.openmini_qmm_soa_bytes(2, 10, (1 << 48) + 1, ctypes.byref(out)) == _native.ERR_INVALID_PARAM

@@ -276,3 +276,18 @@ def test_dequant_beyond_one_launch_slice(qmm, orc, qtype):
             assert np.all(tail == 0.0) and not np.any(np.signbit(tail))
     d_in.free()
     d_out.free()
+
+
+@pytest.mark.parametrize("qtype", [0, 1, 2, 3, 7, 12, 24])
+def test_convert_to_soa_layout_matches_oracle(qmm, orc, qtype):
+    """convert_to_soa_layout on the GPU (quant_simd.rs:3245-3397) byte for byte against
+    the oracle: whole blocks, a ragged n, inputs cut inside a block and inside an fp16
+    field, n larger than the input, and empty input."""
+    bpb = {0: 4, 1: 2, 2: 18, 3: 20, 7: 34, 12: 144, 24: 1}[qtype]
+    nblk = 4099
+    raw = np.random.default_rng(qtype + 40).integers(0, 256, nblk * bpb, dtype=np.uint8)
+    print(f"convert_to_soa type={qtype} bytes={raw.size}", flush=True)
+    for data, n in ((raw, nblk * 32), (raw, nblk * 32 - 7), (raw[: 17 * bpb + 1], 17 * 32),
+                    (raw[: 17 * bpb + 3], 40 * 32), (raw, nblk * 64), (raw[:0], 64), (raw, 0)):
+        got = qmm.convert_to_soa_layout(data, qtype, n)
+        assert np.array_equal(got, orc.convert_to_soa(qtype, data, n)), (qtype, data.size, n)

@@ -197,18 +197,43 @@ def test_reference_soa_kats(orc, case):
         assert bytes(soa[: len(p)]) == p
 
 
-@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, 3])
 def test_soa_is_the_position_major_permutation(orc, qtype):
-    bpb = 18 if qtype == Q4_0 else 34
+    """numpy restatement: the fp16 fields of every block (scale; Q4_1 also min) field by
+    field, then the code bytes position-major; a short input reads as zeros."""
+    bpb = {Q4_0: 18, Q8_0: 34, 3: 20}[qtype]
+    hdr = 4 if qtype == 3 else 2
     nblk = 7
     raw = np.random.default_rng(5).integers(0, 256, nblk * bpb, dtype=np.uint8)
     soa = orc.convert_to_soa(qtype, raw, nblk * 32)
     blocks = raw.reshape(nblk, bpb)
-    assert np.array_equal(soa[: 2 * nblk].reshape(nblk, 2), blocks[:, :2])
-    assert np.array_equal(soa[2 * nblk:].reshape(bpb - 2, nblk), blocks[:, 2:].T)
-    short = orc.convert_to_soa(qtype, raw[: bpb + 3], 2 * 32)  # missing bytes read as 0
-    assert short.size == 2 * bpb and short[2] == raw[bpb] and short[3] == raw[bpb + 1]
+    fields = np.concatenate([blocks[:, f:f + 2].reshape(-1) for f in range(0, hdr, 2)])
+    assert np.array_equal(soa[: hdr * nblk], fields)
+    assert np.array_equal(soa[hdr * nblk:].reshape(bpb - hdr, nblk), blocks[:, hdr:].T)
+    # ragged n: ceil(n / 32) blocks; code bytes past the input are zeros, and an fp16
+    # field is copied only when both of its bytes are there (quant_simd.rs:3339-3343)
+    for cut in (bpb + 1, bpb + 3):
+        short = orc.convert_to_soa(qtype, raw[:cut], 2 * 32 - 5)
+        padded = np.concatenate([raw[:cut], np.zeros(2 * bpb - cut, np.uint8)]).reshape(2, bpb)
+        fld = [padded[:, f:f + 2].copy() for f in range(0, hdr, 2)]
+        for i, f in enumerate(range(0, hdr, 2)):
+            if bpb + f + 2 > cut:
+                fld[i][1] = 0
+        want = np.concatenate([x.reshape(-1) for x in fld] + [padded[:, hdr:].T.reshape(-1)])
+        assert np.array_equal(short, want), cut
     assert orc.convert_to_soa(qtype, b"", 32).size == 0
+    assert orc.convert_to_soa(qtype, raw, 0).size == 0
+
+
+def test_soa_copy_arms(orc):
+    """F32 / F16: the first min(n * element size, len) bytes; other types: the input
+    as it is (quant_simd.rs:3257-3292)."""
+    raw = np.random.default_rng(6).integers(0, 256, 103, dtype=np.uint8)
+    assert np.array_equal(orc.convert_to_soa(0, raw, 10), raw[:40])
+    assert np.array_equal(orc.convert_to_soa(0, raw, 1000), raw)
+    assert np.array_equal(orc.convert_to_soa(1, raw, 7), raw[:14])
+    for t in (10, 12, 14, 8, 24):
+        assert np.array_equal(orc.convert_to_soa(t, raw, 5), raw)
 
 
 # ---- synthetic-weight quantizers ---------------------------------------------------------
