@@ -264,6 +264,71 @@ def cpu_baseline(gemv: dict, seconds: float) -> dict:
     }
 
 
+def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
+    """The load-side rows on the GPU, on one 11008 x 4096 projection:
+    * dequantization of raw GGUF blocks to f32 (quant::dequantize, GpuQuantOps;
+      openmini_qmm_dequantize_any_device) for Q4_0, Q8_0 and Q4_K, graph-replayed over
+      rotated inputs like the GEMV;
+    * the upload of raw Q4_0 blocks already in device memory (openmini_qmm_upload_device:
+      the weight's allocation plus the repack into chunks), timed as whole calls.
+    Bytes counted: GGUF bytes read + bytes written (f32 outputs / chunks)."""
+    from openmini_qmm import _native, synth
+    L = _native.lib()
+    sh = stream.handle
+    n = N * K
+    res = {"dequantize": []}
+    for qtype, name in ((Q4_0, "q4_0"), (Q8_0, "q8_0"), (12, "q4_k")):
+        if qtype == 12:
+            raw = np.random.default_rng(0x5EED0050).integers(0, 256, n // 256 * 144, dtype=np.uint8)
+            raw[1::144] &= 0x7B  # finite fp16 d and dmin
+            raw[3::144] &= 0x7B
+        else:
+            raw = synth.weight_blocks(qtype, N, K, seed=0x5EED0051 + qtype)
+        copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // raw.size))
+        ins = [qmm.DeviceBuffer.from_numpy(raw) for _ in range(copies)]
+        outs = [qmm.DeviceBuffer(n * 4) for _ in range(2)]
+
+        def launch(i):
+            rc = L.openmini_qmm_dequantize_any_device(qtype, ins[i % copies].ptr, raw.size, n, outs[i % 2].ptr, sh)
+            if rc:
+                raise RuntimeError(L.openmini_qmm_last_error().decode())
+
+        for i in range(warmup):
+            launch(i)
+        stream.synchronize()
+        ms = time_steps(launch, steps, sh, hipr) / steps
+        alg = raw.size + n * 4
+        res["dequantize"].append({"workload": f"{name}_dequant_n{N}_k{K}", "unit": "GB/s",
+                                  "value": round(alg / (ms * 1e-3) / 1e9, 2), "kernel_us": round(ms * 1e3, 3),
+                                  "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "alg_bytes_per_step": alg})
+        for b in ins + outs:
+            b.free()
+    raw = synth.weight_blocks(Q4_0, N, K, seed=0x5EED0052)
+    d_raw = qmm.DeviceBuffer.from_numpy(raw)
+    for w in [qmm.QuantizedWeight.from_device(Q4_0, d_raw, raw.size, N, K, sh) for _ in range(3)]:
+        stream.synchronize()
+        w.close()
+    reps = 20
+    hipr.hip().hipDeviceSynchronize()
+    e0, e1 = hipr.Event(), hipr.Event()
+    e0.record(sh)
+    ws = [qmm.QuantizedWeight.from_device(Q4_0, d_raw, raw.size, N, K, sh) for _ in range(reps)]
+    e1.record(sh)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    chunk_bytes = ws[0].info().device_bytes
+    for w in ws:
+        w.close()
+    d_raw.free()
+    alg = raw.size + chunk_bytes
+    res["upload"] = {"workload": f"q4_0_upload_device_n{N}_k{K}", "unit": "GB/s",
+                     "value": round(alg / (ms * 1e-3) / 1e9, 2), "us_per_call": round(ms * 1e3, 3),
+                     "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": alg,
+                     "includes": "the weight's hipMalloc and the repack kernel"}
+    return res
+
+
 def bench_layer(qmm, hipr, stream, steps, warmup, qtype=Q4_0, H=4096, I=11008, seed=0x5EED0010):
     """One Llama-7B decode layer's seven projections at batch 1 (q, k, v, o [H, H];
     gate, up [I, H]; down [H, I]) over distinct layers' weights (>= 1 GiB rotated):
@@ -325,6 +390,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM leg")
     ap.add_argument("--no-layer", action="store_true", help="skip the decode-layer leg")
     ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode legs")
+    ap.add_argument("--no-weight-path", action="store_true", help="skip the dequantize / upload legs")
     ap.add_argument("--eager", action="store_true",
                     help="launch directly instead of replaying a HIP graph (for counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -379,6 +445,13 @@ def main(argv=None) -> int:
                             "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
                             "alg_bytes_per_step": r["alg_bytes_per_step"]})
             log(f"batched {batched[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
+    wpath = None
+    if not args.no_weight_path:
+        wpath = bench_weight_path(qmm, hipr, stream, max(20, args.steps // 4), max(3, args.warmup // 4))
+        for r in wpath["dequantize"]:
+            log(f"dequantize {r['workload']}: {r['kernel_us']:.2f} us, {r['value']:.1f} GB/s")
+        log(f"upload {wpath['upload']['workload']}: {wpath['upload']['us_per_call']:.2f} us per call, "
+            f"{wpath['upload']['value']:.1f} GB/s")
     copy = None
     if args.calibrate_copy:
         copy = copy_calibration(qmm, hipr, stream)
@@ -431,6 +504,8 @@ def main(argv=None) -> int:
         out["prefill_sizes"] = prefill
     if batched:
         out["batched_decode"] = batched
+    if wpath:
+        out["weight_path"] = wpath
     if layer:
         out["decode_layer"] = {
             "workload": "q4_0_llama7b_layer_7proj_b1", "unit": "GB/s",

@@ -122,10 +122,6 @@ hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s);
 // Repacked weight -> f32 [n][k].
 hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s);
 
-// Raw GGUF bytes -> f32 [n_elems] (reads only complete blocks; caller validated size).
-hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, float* out,
-                               hipStream_t s);
-
 // y[batch][n] = x[batch][k] . W^T for 1 <= batch <= kMaxGemvBatch.
 hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hipStream_t s);
 

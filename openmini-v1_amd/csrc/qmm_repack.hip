@@ -139,34 +139,6 @@ __global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __re
     o[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// Raw GGUF blocks -> f32[n] (GpuQuantOps path).  One thread per 8-element group
-// of a block; byte loads because 18/34-byte blocks are only byte aligned in
-// general.  Elements >= n are not written (quant.rs:175-177).
-template <int kBPB>
-__global__ __launch_bounds__(256) void dequant_gguf_kernel(const uint8_t* __restrict__ gguf,
-                                                           size_t n, float* __restrict__ out) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t blk = g >> 2;
-    const int grp = (int)(g & 3);
-    const int64_t e0 = blk * kQK + grp * 8;
-    if (e0 >= (int64_t)n) return;
-    const uint8_t* b = gguf + blk * kBPB;
-    const float d = f16_bits_to_f32((uint16_t)(b[0] | (b[1] << 8)));
-    const uint8_t* qs = b + 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int e = grp * 8 + i;
-        float v;
-        if constexpr (kBPB == 18) {
-            const int q = (int)q4_code(qs, e) - 8;
-            v = (float)q * d;
-        } else {
-            v = (float)(int8_t)qs[e] * d;
-        }
-        if (e0 + i < (int64_t)n) out[e0 + i] = v;
-    }
-}
-
 // ---- the other GGUF layouts of quant::dequantize (quant.rs:56-79, 216-800) -----------
 //
 // One thread per 8 consecutive outputs.  Each value follows the reference's formula
@@ -278,6 +250,34 @@ __device__ __forceinline__ float elem(const uint8_t* b, int i) {
     return elem_q8_k(b, i);
 }
 
+// Q4_0 / Q8_0 (quant.rs:152-195, 282-316) from halfword loads: blocks of 18 / 34 bytes
+// start on even addresses, so the scale and each code pair are 2-byte aligned.
+template <int kType>
+__device__ __forceinline__ void eight_q(const uint8_t* b, int i0, float* v) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+    const float d = f16_bits_to_f32(h[0]);
+    if constexpr (kType == OPENMINI_QMM_Q4_0) {
+        // elements 2j (high nibble) and 2j + 1 (low nibble) of code byte j
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t w = h[1 + i0 / 4 + p];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t c = (w >> (8 * t)) & 0xFFu;
+                v[4 * p + 2 * t] = (float)((int)(c >> 4) - 8) * d;
+                v[4 * p + 2 * t + 1] = (float)((int)(c & 0x0Fu) - 8) * d;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t w = h[1 + i0 / 2 + p];
+            v[2 * p] = (float)(int8_t)(w & 0xFFu) * d;
+            v[2 * p + 1] = (float)(int8_t)(w >> 8) * d;
+        }
+    }
+}
+
 template <int kType>
 __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __restrict__ gguf, size_t n,
                                                              size_t avail_blocks, float* __restrict__ out) {
@@ -287,10 +287,28 @@ __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __re
     const size_t blk = e0 / L::kQ;
     const int i0 = (int)(e0 % L::kQ);
     const uint8_t* b = gguf + blk * L::kB;
-    const bool have = blk < avail_blocks;
+    float v[8];
+    if (blk < avail_blocks) {
+        if constexpr (kType == OPENMINI_QMM_Q4_0 || kType == OPENMINI_QMM_Q8_0) {
+            eight_q<kType>(b, i0, v);
+        } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        if (e0 + j < n) out[e0 + j] = have ? elem<kType>(b, i0 + j) : 0.0f;
+            for (int j = 0; j < 8; ++j) v[j] = elem<kType>(b, i0 + j);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    // all values first, then the stores: two 16-byte stores for a whole, aligned slot
+    float* o = out + e0;
+    if (e0 + 8 <= n && ((uintptr_t)o & 15) == 0) {
+        reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (e0 + j < n) o[j] = v[j];
+    }
 }
 
 // F32 / F16 arms (quant.rs:95-133): element-wise, missing bytes give 0.
@@ -369,18 +387,6 @@ hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s) {
     else
         hipLaunchKernelGGL(dequant_weight_kernel<false>, grid, dim3(256), 0, s, w.chunks, nwords,
                            w.nb, w.groups, out);
-    return hipGetLastError();
-}
-
-hipError_t launch_dequant_gguf(int type, const uint8_t* gguf, size_t n_elems, float* out,
-                               hipStream_t s) {
-    if (n_elems == 0) return hipSuccess;
-    const int64_t nblocks = (int64_t)((n_elems + kQK - 1) / kQK);
-    const dim3 grid(grid_for(nblocks * 4, 256));
-    if (type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(dequant_gguf_kernel<18>, grid, dim3(256), 0, s, gguf, n_elems, out);
-    else
-        hipLaunchKernelGGL(dequant_gguf_kernel<34>, grid, dim3(256), 0, s, gguf, n_elems, out);
     return hipGetLastError();
 }
 
