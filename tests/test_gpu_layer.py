@@ -81,13 +81,20 @@ def test_ffn_gate_up_gemv(qmm, orc, qtype, N, K, B):
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 @pytest.mark.parametrize("N,K,M", [(11008, 4096, 128), (11008, 4096, 512), (1000, 2080, 77), (48, 96, 300)])
 def test_ffn_gate_up_bf16(qmm, orc, qtype, N, K, M):
+    """Prefill FFN hidden state through the GEMM's SwiGLU epilogue.  At the full
+    Llama-7B sizes the fp64 oracle runs on a sample of rows (first, last and random
+    ones; a row of h depends only on its own x row); every row is still checked
+    against the composition of the two plain GEMMs below."""
     print(f"ffn_gate_up_bf16 type={qtype} N={N} K={K} M={M}", flush=True)
     (wg, bg), (wu, bu) = _weights(qmm, qtype, ((N, K), (N, K)), seed=0x9500 + N + M)
     xb = synth.to_bf16_bits(synth.normal(0x9501 + M, (M, K), 1.0))
     dx, dh = qmm.DeviceBuffer.from_numpy(xb), qmm.DeviceBuffer(M * N * 4)
     qmm.ffn_gate_up_bf16(wg, wu, dx, dh, M)
     h = dh.download(np.float32, (M, N))
-    assert_parity(h, orc.ffn_hidden_bf16x_f64(qtype, bg, bu, N, K, xb), TOL, "hidden bf16")
+    rows = np.arange(M)
+    if M * N * K > (1 << 31):
+        rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M + N).integers(0, M, 6)]))
+    assert_parity(h[rows], orc.ffn_hidden_bf16x_f64(qtype, bg, bu, N, K, xb[rows]), TOL, "hidden bf16")
     # composition against the plain GEMM of each weight
     dg = qmm.DeviceBuffer(M * N * 4)
     wg.gemm_bf16(dx, dg, M)
