@@ -39,6 +39,13 @@ Q4_0, Q8_0 = 2, 7
 MALL_DEFEAT_BYTES = 1 << 30
 
 
+def sha256(a: np.ndarray) -> str:
+    """SHA-256 of a synthetic input buffer's bytes, recorded so runs can be compared
+    input for input."""
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -105,7 +112,7 @@ def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed
         "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
         "gbs_wall": alg_bytes * steps / (total_ms * 1e-3) / 1e9,
         "gbs_kernel": alg_bytes / (per_launch_ms * 1e-3) / 1e9,
-        "blocks": blocks, "x": x,
+        "blocks": blocks, "x": x, "sha256": {"weight": sha256(blocks), "x": sha256(x)},
     }
     for w in ws:
         w.close()
@@ -136,6 +143,7 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
         w.close()
     return {
         "N": N, "K": K, "M": M, "weight_copies": copies,
+        "sha256": {"weight": sha256(blocks), "x_bf16": sha256(xb)},
         "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
         "tflops_wall": flops * steps / (total_ms * 1e-3) / 1e12,
         "tflops_kernel": flops / (per_launch_ms * 1e-3) / 1e12,
@@ -301,7 +309,7 @@ def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
         res["dequantize"].append({"workload": f"{name}_dequant_n{N}_k{K}", "unit": "GB/s",
                                   "value": round(alg / (ms * 1e-3) / 1e9, 2), "kernel_us": round(ms * 1e3, 3),
                                   "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                  "alg_bytes_per_step": alg})
+                                  "alg_bytes_per_step": alg, "sha256": {"gguf": sha256(raw)}})
         for b in ins + outs:
             b.free()
     raw = synth.weight_blocks(Q4_0, N, K, seed=0x5EED0052)
@@ -325,7 +333,8 @@ def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
     res["upload"] = {"workload": f"q4_0_upload_device_n{N}_k{K}", "unit": "GB/s",
                      "value": round(alg / (ms * 1e-3) / 1e9, 2), "us_per_call": round(ms * 1e3, 3),
                      "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": alg,
-                     "includes": "the weight's hipMalloc and the repack kernel"}
+                     "includes": "the weight's hipMalloc and the repack kernel",
+                     "sha256": {"gguf": sha256(raw)}}
     return res
 
 
@@ -366,7 +375,8 @@ def bench_layer(qmm, hipr, stream, steps, warmup, qtype=Q4_0, H=4096, I=11008, s
         u.gemv(dx, du, 1, sh)
         d.gemv(dh, dd, 1, sh)
 
-    res = {"H": H, "I": I, "layer_bytes": layer_bytes, "layers": copies}
+    res = {"H": H, "I": I, "layer_bytes": layer_bytes, "layers": copies,
+           "sha256": {"weights": sha256(np.concatenate(blocks)), "x": sha256(x)}}
     for name, fn in (("grouped", grouped), ("separate", separate)):
         for i in range(warmup):
             fn(i)
@@ -426,7 +436,7 @@ def main(argv=None) -> int:
             r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 8), max(3, args.warmup // 4), M=m)
             prefill.append({"workload": f"q8_0_gemm_n11008_k4096_m{m}_bf16x", "unit": "TFLOP/s",
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
-                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4)})
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
             log(f"q8_0 gemm M={m}: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
     layer = None
     if not args.no_layer:
@@ -443,7 +453,7 @@ def main(argv=None) -> int:
             batched.append({"workload": f"{name}_gemv_n{n}_k{k}_b{b}", "unit": "GB/s",
                             "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                             "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
-                            "alg_bytes_per_step": r["alg_bytes_per_step"]})
+                            "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})
             log(f"batched {batched[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
     wpath = None
     if not args.no_weight_path:
@@ -478,14 +488,14 @@ def main(argv=None) -> int:
         "config": {"workload": workload, "N": g["N"], "K": g["K"], "batch": 1,
                    "weight": "Q4_0 from N(0, 0.02)", "x": "f32 N(0, 1)",
                    "weight_copies": g["weight_copies"], "rotated_bytes": g["rotated_bytes"],
-                   "alg_bytes_per_step": g["alg_bytes_per_step"]},
+                   "alg_bytes_per_step": g["alg_bytes_per_step"], "sha256": g["sha256"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "kernel_us": round(g["kernel_ms"] * 1e3, 3)},
         "pct_of_hbm_peak_wall": round(100.0 * g["gbs_wall"] / HBM_PEAK_GBS, 2),
         "down_proj": {"workload": "q4_0_gemv_n4096_k11008_b1", "value": round(down["gbs_wall"], 2),
                       "unit": "GB/s", "kernel_gbs": round(down["gbs_kernel"], 2),
-                      "kernel_us": round(down["kernel_ms"] * 1e3, 3)},
+                      "kernel_us": round(down["kernel_ms"] * 1e3, 3), "sha256": down["sha256"]},
         "cpu_baseline": cpu,
     }
     if copy:
@@ -493,6 +503,7 @@ def main(argv=None) -> int:
     if gemm:
         out["gemm"] = {
             "metric": "Q8_0 GEMM TFLOP/s M=512", "workload": "q8_0_gemm_n11008_k4096_m512_bf16x",
+            "sha256": gemm["sha256"],
             "value": round(gemm["tflops_wall"], 2), "unit": "TFLOP/s", "dtype": "bf16",
             "ms_per_step": round(gemm["ms_per_step"], 6),
             "roofline": {"bound": "mfma", "achieved": round(gemm["tflops_kernel"], 2),
@@ -512,7 +523,7 @@ def main(argv=None) -> int:
             "value": round(layer["grouped_gbs"], 2), "us_per_layer": round(layer["grouped_us"], 3),
             "launches": 4, "separate_gbs": round(layer["separate_gbs"], 2),
             "separate_us_per_layer": round(layer["separate_us"], 3), "separate_launches": 7,
-            "layer_bytes": layer["layer_bytes"], "layers_rotated": layer["layers"],
+            "layer_bytes": layer["layer_bytes"], "layers_rotated": layer["layers"], "sha256": layer["sha256"],
         }
     print(json.dumps(out), flush=True)
     return 0
