@@ -79,10 +79,6 @@ inline int layout_bytes_per_block(int type) {
     default: return 0;
     }
 }
-inline int code_bytes_per_block(int type) {
-    return type == OPENMINI_QMM_Q4_0 ? 16 : type == OPENMINI_QMM_Q8_0 ? 32 : 0;
-}
-
 constexpr int kTileRows = 16;   // rows per tile
 constexpr int kTileBlocks = 4;  // blocks per group
 constexpr int kTileEntries = kTileRows * kTileBlocks;  // slots per chunk

@@ -221,9 +221,6 @@ __device__ float elem_q3_k(const uint8_t* b, int i) {
 }
 // quant.rs:768-800
 __device__ float elem_q8_k(const uint8_t* b, int i) { return (float)(int8_t)b[2 + i] * f16_at(b); }
-// quant.rs:152-195, 282-316
-__device__ float elem_q4_0(const uint8_t* b, int i) { return (float)((int)q4_code(b + 2, i) - 8) * f16_at(b); }
-__device__ float elem_q8_0(const uint8_t* b, int i) { return (float)(int8_t)b[2 + i] * f16_at(b); }
 
 template <int kType>
 struct Layout;
@@ -239,8 +236,6 @@ template <> struct Layout<OPENMINI_QMM_Q8_K> { static constexpr int kQ = 256, kB
 
 template <int kType>
 __device__ __forceinline__ float elem(const uint8_t* b, int i) {
-    if constexpr (kType == OPENMINI_QMM_Q4_0) return elem_q4_0(b, i);
-    if constexpr (kType == OPENMINI_QMM_Q8_0) return elem_q8_0(b, i);
     if constexpr (kType == OPENMINI_QMM_Q4_1) return elem_q4_1(b, i);
     if constexpr (kType == OPENMINI_QMM_Q2_K) return elem_q2_k(b, i);
     if constexpr (kType == OPENMINI_QMM_Q3_K) return elem_q3_k(b, i);
