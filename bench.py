@@ -401,6 +401,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-layer", action="store_true", help="skip the decode-layer leg")
     ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode legs")
     ap.add_argument("--no-weight-path", action="store_true", help="skip the dequantize / upload legs")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the other batch-1 decode shapes")
     ap.add_argument("--eager", action="store_true",
                     help="launch directly instead of replaying a HIP graph (for counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -455,6 +456,20 @@ def main(argv=None) -> int:
                             "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
                             "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})
             log(f"batched {batched[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
+    shapes = []
+    if not args.no_shapes:
+        # the remaining decode configs of the measurement table (batch 1)
+        for qtype, n, k, seed in ((Q4_0, 4096, 4096, 0x5EED0061), (Q8_0, 11008, 4096, 0x5EED0062),
+                                  (Q8_0, 4096, 11008, 0x5EED0063), (Q4_0, 8192, 8192, 0x5EED0064),
+                                  (Q4_0, 28672, 8192, 0x5EED0065), (Q4_0, 8192, 28672, 0x5EED0066)):
+            r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
+                           qtype=qtype, batch=1, seed=seed)
+            name = "q4_0" if qtype == Q4_0 else "q8_0"
+            shapes.append({"workload": f"{name}_gemv_n{n}_k{k}_b1", "unit": "GB/s",
+                           "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                           "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
+                           "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})
+            log(f"decode {shapes[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
     wpath = None
     if not args.no_weight_path:
         wpath = bench_weight_path(qmm, hipr, stream, max(20, args.steps // 4), max(3, args.warmup // 4))
@@ -515,6 +530,8 @@ def main(argv=None) -> int:
         out["prefill_sizes"] = prefill
     if batched:
         out["batched_decode"] = batched
+    if shapes:
+        out["decode_shapes"] = shapes
     if wpath:
         out["weight_path"] = wpath
     if layer:
