@@ -294,11 +294,13 @@ __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __re
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = 0.0f;
     }
-    // all values first, then the stores: two 16-byte stores for a whole, aligned slot
+    // all values first, then the stores: two 16-byte streaming (nontemporal) stores
+    // for a whole, aligned slot -- the output is written once and not read back here
     float* o = out + e0;
     if (e0 + 8 <= n && ((uintptr_t)o & 15) == 0) {
-        reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
-        reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
+        typedef float f32x4v __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(o));
+        __builtin_nontemporal_store(f32x4v{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4v*>(o) + 1);
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
