@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __re
 
 // ---- the other GGUF layouts of quant::dequantize (quant.rs:56-79, 216-800) -----------
 //
-// One thread per 8 consecutive outputs.  Each value follows the reference's formula
+// Each value follows the reference's formula
 // with one IEEE operation per Rust operator, in its order, and no contraction: every
 // product in these formulas is exact in binary32 (at most 23 significant bits), so
 // only the final additions round and the results are bit-identical, signed zeros
@@ -245,66 +245,69 @@ __device__ __forceinline__ float elem(const uint8_t* b, int i) {
     return elem_q8_k(b, i);
 }
 
-// Q4_0 / Q8_0 (quant.rs:152-195, 282-316) from halfword loads: blocks of 18 / 34 bytes
-// start on even addresses, so the scale and each code pair are 2-byte aligned.
+// Four outputs at element e (a multiple of 4) of one block.  Q4_0 / Q8_0
+// (quant.rs:152-195, 282-316) read the scale and codes as halfwords: blocks of 18 / 34
+// bytes start on even addresses.  Past n or past the blocks given: zeros.
 template <int kType>
-__device__ __forceinline__ void eight_q(const uint8_t* b, int i0, float* v) {
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
-    const float d = f16_bits_to_f32(h[0]);
+__device__ __forceinline__ void four_values(const uint8_t* __restrict__ gguf, size_t e, size_t n,
+                                            size_t avail_blocks, float* v) {
+    using L = Layout<kType>;
+    const size_t blk = e / L::kQ;
+    const int i0 = (int)(e % L::kQ);
+    if (e >= n || blk >= avail_blocks) {
+        v[0] = v[1] = v[2] = v[3] = 0.0f;
+        return;
+    }
+    const uint8_t* b = gguf + blk * L::kB;
     if constexpr (kType == OPENMINI_QMM_Q4_0) {
-        // elements 2j (high nibble) and 2j + 1 (low nibble) of code byte j
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+        const float d = f16_bits_to_f32(h[0]);
+        const uint32_t w = h[1 + i0 / 4];  // elements 2j (high nibble), 2j + 1 (low) of byte j
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t c = (w >> (8 * t)) & 0xFFu;
+            v[2 * t] = (float)((int)(c >> 4) - 8) * d;
+            v[2 * t + 1] = (float)((int)(c & 0x0Fu) - 8) * d;
+        }
+    } else if constexpr (kType == OPENMINI_QMM_Q8_0) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+        const float d = f16_bits_to_f32(h[0]);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            const uint32_t w = h[1 + i0 / 4 + p];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint32_t c = (w >> (8 * t)) & 0xFFu;
-                v[4 * p + 2 * t] = (float)((int)(c >> 4) - 8) * d;
-                v[4 * p + 2 * t + 1] = (float)((int)(c & 0x0Fu) - 8) * d;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
             const uint32_t w = h[1 + i0 / 2 + p];
             v[2 * p] = (float)(int8_t)(w & 0xFFu) * d;
             v[2 * p + 1] = (float)(int8_t)(w >> 8) * d;
         }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = elem<kType>(b, i0 + j);
     }
 }
 
+// A wave covers 512 consecutive outputs: lane l computes the four at 4 l and the four
+// at 256 + 4 l, so each of its two store instructions writes one contiguous 1 KB span
+// (whole 128-byte lines).  Values are computed before the stores, which are streaming
+// (nontemporal): the output is written once and not read back here.
 template <int kType>
 __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __restrict__ gguf, size_t n,
                                                              size_t avail_blocks, float* __restrict__ out) {
-    using L = Layout<kType>;
-    const size_t e0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-    if (e0 >= n) return;
-    const size_t blk = e0 / L::kQ;
-    const int i0 = (int)(e0 % L::kQ);
-    const uint8_t* b = gguf + blk * L::kB;
-    float v[8];
-    if (blk < avail_blocks) {
-        if constexpr (kType == OPENMINI_QMM_Q4_0 || kType == OPENMINI_QMM_Q8_0) {
-            eight_q<kType>(b, i0, v);
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t ea = (t >> 6) * 512 + (t & 63) * 4;
+    if (ea >= n) return;
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    const bool aligned = ((uintptr_t)out & 15) == 0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const size_t e = ea + 256 * half;
+        float v[4];
+        four_values<kType>(gguf, e, n, avail_blocks, v);
+        if (aligned && e + 4 <= n) {
+            __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(out + e));
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = elem<kType>(b, i0 + j);
+            for (int j = 0; j < 4; ++j)
+                if (e + j < n) out[e + j] = v[j];
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
-    // all values first, then the stores: two 16-byte streaming (nontemporal) stores
-    // for a whole, aligned slot -- the output is written once and not read back here
-    float* o = out + e0;
-    if (e0 + 8 <= n && ((uintptr_t)o & 15) == 0) {
-        typedef float f32x4v __attribute__((ext_vector_type(4)));
-        __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(o));
-        __builtin_nontemporal_store(f32x4v{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4v*>(o) + 1);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (e0 + j < n) o[j] = v[j];
     }
 }
 
@@ -434,7 +437,7 @@ hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, si
                            bytes / esz, type == OPENMINI_QMM_F16 ? 1 : 0, out);
         return hipGetLastError();
     }
-    const dim3 grid(grid_for((int64_t)((n_elems + 7) / 8), 256));
+    const dim3 grid(grid_for((int64_t)((n_elems + 511) / 512 * 64), 256));  // a wave per 512 outputs
     switch (type) {
 #define QMM_LAYOUT_CASE(T)                                                                              \
     case T:                                                                                             \
