@@ -311,19 +311,55 @@ __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __re
     }
 }
 
-// F32 / F16 arms (quant.rs:95-133): element-wise, missing bytes give 0.
+// F32 / F16 arms (quant.rs:95-133): element-wise, missing bytes give 0.  Same wave
+// layout as the block arms (512 outputs per wave, contiguous 1 KB store spans).  With
+// a 16-byte aligned source, a lane's four inputs come in one load; otherwise byte by
+// byte.
+template <int kEsz>
 __global__ __launch_bounds__(256) void dequant_plain_kernel(const uint8_t* __restrict__ src, size_t n,
-                                                            size_t avail, int f16, float* __restrict__ out) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    if (i >= avail) {
-        out[i] = 0.0f;
-    } else if (f16) {
-        out[i] = f16_at(src + 2 * i);
-    } else {
-        uint32_t v = (uint32_t)src[4 * i] | ((uint32_t)src[4 * i + 1] << 8) | ((uint32_t)src[4 * i + 2] << 16) |
-                     ((uint32_t)src[4 * i + 3] << 24);
-        out[i] = __uint_as_float(v);
+                                                            size_t avail, float* __restrict__ out) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t ea = (t >> 6) * 512 + (t & 63) * 4;
+    if (ea >= n) return;
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    const bool src16 = ((uintptr_t)src & 15) == 0, out16 = ((uintptr_t)out & 15) == 0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const size_t e = ea + 256 * half;
+        float v[4];
+        if (src16 && e + 4 <= avail) {
+            if constexpr (kEsz == 4) {
+                const float4 q = *reinterpret_cast<const float4*>(src + 4 * e);
+                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            } else {
+                const uint2 q = *reinterpret_cast<const uint2*>(src + 2 * e);
+                v[0] = f16_bits_to_f32((uint16_t)(q.x & 0xFFFFu));
+                v[1] = f16_bits_to_f32((uint16_t)(q.x >> 16));
+                v[2] = f16_bits_to_f32((uint16_t)(q.y & 0xFFFFu));
+                v[3] = f16_bits_to_f32((uint16_t)(q.y >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const size_t i = e + j;
+                if (i >= avail) {
+                    v[j] = 0.0f;
+                } else if constexpr (kEsz == 2) {
+                    v[j] = f16_at(src + 2 * i);
+                } else {
+                    const uint8_t* p = src + 4 * i;
+                    v[j] = __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                                           ((uint32_t)p[3] << 24));
+                }
+            }
+        }
+        if (out16 && e + 4 <= n) {
+            __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(out + e));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (e + j < n) out[e + j] = v[j];
+        }
     }
 }
 
@@ -432,9 +468,11 @@ hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, si
     }
     if (n_elems == 0) return hipSuccess;
     if (type == OPENMINI_QMM_F32 || type == OPENMINI_QMM_F16) {
-        const size_t esz = type == OPENMINI_QMM_F16 ? 2 : 4;
-        hipLaunchKernelGGL(dequant_plain_kernel, dim3(grid_for((int64_t)n_elems, 256)), dim3(256), 0, s, gguf, n_elems,
-                           bytes / esz, type == OPENMINI_QMM_F16 ? 1 : 0, out);
+        const dim3 grid(grid_for((int64_t)((n_elems + 511) / 512 * 64), 256));  // a wave per 512 outputs
+        if (type == OPENMINI_QMM_F16)
+            hipLaunchKernelGGL(dequant_plain_kernel<2>, grid, dim3(256), 0, s, gguf, n_elems, bytes / 2, out);
+        else
+            hipLaunchKernelGGL(dequant_plain_kernel<4>, grid, dim3(256), 0, s, gguf, n_elems, bytes / 4, out);
         return hipGetLastError();
     }
     const dim3 grid(grid_for((int64_t)((n_elems + 511) / 512 * 64), 256));  // a wave per 512 outputs
