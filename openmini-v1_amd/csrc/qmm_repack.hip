@@ -99,48 +99,48 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
     if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
-// Chunked weight -> f32 [n][k].  One thread per 8 consecutive elements of a row
-// (one Q4_0 code word / two Q8_0 code words); stores are 2 x float4, contiguous
-// across the wave.
+// Chunked weight -> f32 [n][k] (8 * nwords outputs, row-major; one code word = 8
+// consecutive elements of a row).  A wave covers 512 consecutive outputs: lane l
+// decodes the half-word of four at 4 l and the one at 256 + 4 l, so each of its two
+// 16-byte streaming stores is one contiguous 1 KB span.
 template <bool kQ4>
 __global__ __launch_bounds__(256) void dequant_weight_kernel(const uint8_t* __restrict__ chunks,
                                                              int64_t nwords, int64_t nb,
                                                              int64_t groups, float* __restrict__ out) {
     constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kChunk = chunk_bytes_for(kQ4);
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= nwords) return;
-    const int64_t row = g / (nb * 4);
-    const int64_t rem = g - row * nb * 4;
-    const int64_t blk = rem >> 2;
-    const uint8_t* chunk = chunks + chunk_of(row, blk, groups) * kChunk;
-    const int e = slot_of(row, blk);
-    const int j = (int)(rem & 3);
-    const float d = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(chunk + kTileEntries * kCB)[e]);
-    float v[8];
-    if constexpr (kQ4) {
-        const uint32_t w = reinterpret_cast<const uint32_t*>(chunk + e * 16)[j];
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t ea = (t >> 6) * 512 + (t & 63) * 4, total = nwords * 8;
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // sign-extend the nibble to (q - 8) exactly, then one fp32 multiply, as quant.rs:190
-            v[i] = (float)((int)(w << (28 - 8 * i)) >> 28) * d;
-            v[4 + i] = (float)((int)(w << (24 - 8 * i)) >> 28) * d;
-        }
-    } else {
-        const uint2 w = reinterpret_cast<const uint2*>(chunk + e * 32)[j];
+    for (int half = 0; half < 2; ++half) {
+        const int64_t e = ea + 256 * half;  // a multiple of 4; total is a multiple of 8
+        if (e >= total) return;
+        const int64_t g = e >> 3;
+        const int hi = (int)((e >> 2) & 1);  // elements 4..7 of the word
+        const int64_t row = g / (nb * 4);
+        const int64_t rem = g - row * nb * 4;
+        const int64_t blk = rem >> 2;
+        const uint8_t* chunk = chunks + chunk_of(row, blk, groups) * kChunk;
+        const int slot = slot_of(row, blk);
+        const int j = (int)(rem & 3);
+        const float d = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(chunk + kTileEntries * kCB)[slot]);
+        float v[4];
+        if constexpr (kQ4) {
+            const uint32_t w = reinterpret_cast<const uint32_t*>(chunk + slot * 16)[j];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = (float)(int8_t)(w.x >> (8 * i)) * d;
-            v[4 + i] = (float)(int8_t)(w.y >> (8 * i)) * d;
+            for (int i = 0; i < 4; ++i)  // sign-extend the nibble to (q - 8) exactly, one fp32 multiply (quant.rs:190)
+                v[i] = (float)((int)(w << ((hi ? 24 : 28) - 8 * i)) >> 28) * d;
+        } else {
+            const uint2 w2 = reinterpret_cast<const uint2*>(chunk + slot * 32)[j];
+            const uint32_t w = hi ? w2.y : w2.x;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = (float)(int8_t)(w >> (8 * i)) * d;
         }
+        __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(out + e));
     }
-    float4* o = reinterpret_cast<float4*>(out) + 2 * g;
-    o[0] = make_float4(v[0], v[1], v[2], v[3]);
-    o[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// ---- the other GGUF layouts of quant::dequantize (quant.rs:56-79, 216-800) -----------
-//
 // Each value follows the reference's formula
 // with one IEEE operation per Rust operator, in its order, and no contraction: every
 // product in these formulas is exact in binary32 (at most 23 significant bits), so
@@ -416,7 +416,7 @@ hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
 hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s) {
     const int64_t nwords = w.n * w.nb * 4;
     if (nwords == 0) return hipSuccess;
-    const dim3 grid(grid_for(nwords, 256));
+    const dim3 grid(grid_for((nwords * 8 + 511) / 512 * 64, 256));  // a wave per 512 outputs
     if (w.type == OPENMINI_QMM_Q4_0)
         hipLaunchKernelGGL(dequant_weight_kernel<true>, grid, dim3(256), 0, s, w.chunks, nwords,
                            w.nb, w.groups, out);
