@@ -275,7 +275,7 @@ def cpu_baseline(gemv: dict, seconds: float) -> dict:
 def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
     """The load-side rows on the GPU, on one 11008 x 4096 projection:
     * dequantization of raw GGUF blocks to f32 (quant::dequantize, GpuQuantOps;
-      openmini_qmm_dequantize_any_device) for Q4_0, Q8_0 and Q4_K, graph-replayed over
+      openmini_qmm_dequantize_any_device) for Q4_0, Q8_0, Q4_K and F16, graph-replayed over
       rotated inputs like the GEMV;
     * the upload of raw Q4_0 blocks already in device memory (openmini_qmm_upload_device:
       the weight's allocation plus the repack into chunks), timed as whole calls.
@@ -285,8 +285,11 @@ def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
     sh = stream.handle
     n = N * K
     res = {"dequantize": []}
-    for qtype, name in ((Q4_0, "q4_0"), (Q8_0, "q8_0"), (12, "q4_k")):
-        if qtype == 12:
+    for qtype, name in ((Q4_0, "q4_0"), (Q8_0, "q8_0"), (12, "q4_k"), (1, "f16")):
+        if qtype == 1:
+            raw = np.random.default_rng(0x5EED0053).integers(0, 256, n * 2, dtype=np.uint8)
+            raw[1::2] &= 0x7B  # finite halves
+        elif qtype == 12:
             raw = np.random.default_rng(0x5EED0050).integers(0, 256, n // 256 * 144, dtype=np.uint8)
             raw[1::144] &= 0x7B  # finite fp16 d and dmin
             raw[3::144] &= 0x7B
