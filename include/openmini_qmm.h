@@ -338,6 +338,14 @@ int openmini_qmm_stream_synchronize(void* stream);
  * of the GEMV are scaled against.  No counterpart in the reference. */
 int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void* stream);
 
+/* Single-launch floor: a read-only streaming kernel over `bytes` (multiple of 16,
+ * 16-byte aligned source) on `stream`, 16-byte loads, workgroups of 512 lanes over
+ * consecutive 32 KB spans.  Nothing is written in practice; d_sink (4 bytes, 4-byte
+ * aligned) receives a word only if the data fold hits a sentinel.  The time a
+ * read-bound kernel of that many bytes cannot beat in one launch; the decode GEMV
+ * is measured against it.  No counterpart in the reference. */
+int openmini_qmm_stream_read(const void* d_src, size_t bytes, void* d_sink, void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

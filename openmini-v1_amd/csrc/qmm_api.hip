@@ -716,4 +716,13 @@ int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void*
     return ok();
 }
 
+int openmini_qmm_stream_read(const void* d_src, size_t bytes, void* d_sink, void* stream) {
+    if (!d_src || !d_sink) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null pointer");
+    if (bytes % 16 || !aligned16(d_src) || ((uintptr_t)d_sink & 3u))
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "stream_read needs 16-byte sizes and source alignment");
+    hipError_t e = qmm::launch_stream_read(d_src, bytes, static_cast<uint32_t*>(d_sink), as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "stream_read launch");
+    return ok();
+}
+
 }  // extern "C"

@@ -7,18 +7,20 @@
 //
 // Arithmetic: exact integer dot products on the matrix cores.
 //   * Per 32-element block, x is made block-floating: with M the block's max |x| and
-//     2^(e-1) <= M < 2^e, X_k = round-to-nearest-even(x_k * 2^s), s = 22 - e, so
-//     |X_k| <= 2^22 and the error is <= 2^(e-23) (fp32-level relative to the block max).
-//     The rounding is one fp32 add of 1.5 * 2^23: the sum lies in [2^23, 2^24], where
-//     the fp32 spacing is 1, and its bit pattern is 0x4B400000 + X_k.
-//   * X_k = a*2^16 + b*2^8 + c with a, b, c balanced int8 digits; they are the low
-//     three bytes of (X + 0x808080) ^ 0x808080.
+//     2^(e-1) <= M < 2^e, X_k = round-to-nearest-even(x_k * 2^s), s = 30 - e, so
+//     |X_k| < 2^30 and the error is <= 2^(e-31).  Elements within 2^6 of the block
+//     maximum are exact (24 significant bits); smaller ones are rounded 2^-31 below
+//     the maximum, which keeps the error of an outlier's block (an outlier on a
+//     feature the weight row ignores) below the fp32 accumulation error of the
+//     reference's f32 path.
+//   * X_k = sum_h digit_h * 2^(8h), h = 0..3, with balanced int8 digits: the bytes of
+//     (X + 0x80808080) ^ 0x80808080.
 //   * v_mfma_i32_16x16x64_i8 forms sum_k c_k * digit_k exactly in int32, with c_k the
 //     Q8_0 code or 16 (q_k - 8) for Q4_0 (the stored two's-complement nibble moved to
 //     the top of its byte: 1.5 VALU ops per 4 weights).
-//   * Per block: sum_k c_k x_k = 2^-s * (D_c + 2^8 D_b + 2^16 D_a) (each D exact;
-//     the sum in fp32), times the block's fp16 scale (and 1/16 for Q4_0), accumulated
-//     in fp32.
+//   * Per block: sum_k c_k x_k = 2^-s * ((D_0 + 2^8 D_1) + 2^16 (D_2 + 2^8 D_3)) (the
+//     two halves exact in int32, their combination rounded once in fp32), times the
+//     block's fp16 scale (and 1/16 for Q4_0), accumulated in fp32.
 // Versus unpack + convert + FMA on the VALU (about 2.3 instructions per weight, most
 // of the VALU budget at HBM speed), this is well under 1 per weight.
 //
@@ -27,9 +29,9 @@
 // Lane l = 16t + n feeds row n's block-t codes -- exactly slot l of the (row tile,
 // group) chunk, so a wave-wide load of a chunk's codes is one contiguous 1 KB (Q4_0)
 // / 2 KB (Q8_0), followed by the 128 B of its scales.  A row 4t + h holds digit h of
-// block t (other rows and parts zero), so D[4t + h][n] is digit h's block-t dot
-// product for row n, in lane (n, t), register h.  Two MFMAs cover a block's 32
-// elements.
+// block t (other parts zero), so D[4t + h][n] is digit h's block-t dot product for
+// row n, in lane (n, t), register h: the 16 rows are exactly 4 blocks x 4 digits.
+// Two MFMAs cover a block's 32 elements.
 //
 // One launch can serve several weights that share x and K:
 //   * kGroup: up to kMaxGroup weights (q / k / v projections); workgroup i takes
@@ -76,6 +78,14 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
     return v;
 }
 
+// v_cvt_i32_f32: float -> int32, toward zero, saturating (NaN -> 0).  Written out
+// because a C++ conversion of a non-finite or out-of-range float is undefined.
+__device__ __forceinline__ int cvt_i32(float v) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
 // Raw buffer resource (gfx9 descriptor): out-of-range loads return zero, offsets are
 // 32-bit with the uniform part in an SGPR.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -94,8 +104,9 @@ struct GemvGroup {
 // LDS A-fragment slots of one wave for one phase: [p][b][u = block half][t = block
 // slot][h = digit], 16 bytes each, then one zero slot read by lanes whose A fragment
 // is zero.
+constexpr int kDigits = 4;
 template <int B, int P>
-constexpr int kSlots = P * B * 2 * 4 * 3 + 1;
+constexpr int kSlots = P * B * 2 * 4 * kDigits + 1;
 
 // The leading arguments describe weight 0 (and the up weight of a pair) and fit the
 // SGPRs the kernel arguments are preloaded into; `grp` is read only by workgroups of
@@ -159,23 +170,23 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 
     uint4* my_lds = a_lds[wave];
     if (lane == 0) my_lds[kZero] = make_uint4(0, 0, 0, 0);
-    // This lane's A fragment: row m = ln = 4*at + ah of part lt, live iff at == lt, ah < 3.
-    const int ah = ln & 3, at = ln >> 2;
-    const bool a_live = (at == lt) && (ah < 3);
-    const int a_slot = lt * 3 + ah;
+    // This lane's A fragment: row m = ln = 4*at + ah of part lt, live iff at == lt; its
+    // slot (t = at, h = ah) is then slot ln of the block half.
+    const bool a_live = (ln >> 2) == lt;
+    constexpr int kHalfSlots = 4 * kDigits;  // slots of one block half: (t, h)
     // Where this lane writes its two elements' digits: slot (u = ln / 8, t = lt, h),
     // halfword ln % 8 (a slot is 8 halfwords).
-    uint16_t* wr16 = reinterpret_cast<uint16_t*>(my_lds) + ((ln >> 3) * 12 + lt * 3) * 8 + (ln & 7);
+    uint16_t* wr16 =
+        reinterpret_cast<uint16_t*>(my_lds) + ((ln >> 3) * kHalfSlots + lt * kDigits) * 8 + (ln & 7);
 
     float acc[kNW][B];
 #pragma unroll
     for (int nw = 0; nw < kNW; ++nw)
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[nw][b] = 0.0f;
-    // Max of the rounded activations' bit patterns t = 1.5 * 2^23 + X.  Finite x gives
-    // t in [2^23, 2^24] (bits <= 0x4B800000); a NaN or +-inf x makes t NaN or +-inf,
-    // whose bits lie above.  Tracked per batch row: a non-finite row poisons only its
-    // own outputs.
+    // Max of the bit patterns of |x| (they order like unsigned integers): finite x stays
+    // below 0x7F800000, an inf or NaN reaches it.  Tracked per batch row: a non-finite
+    // row poisons only its own outputs.
     uint32_t seen[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) seen[b] = 0;
@@ -190,13 +201,22 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
         float2 xv[P][B];
         uint4 c[kNW][P][kQ4 ? 1 : 2];
         uint32_t sc[kNW][P];
-        // activations first: L2 hits that land before the weights do
+        // activations first: L2 hits that land before the weights do.  The whole offset
+        // goes in the VGPR operand: the raw-buffer range check covers the VGPR offset
+        // but not the SGPR one, so elements past k (a last group of fewer than 4
+        // blocks) get an offset past the range and read zero without touching memory.
+        uint32_t xoff[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const uint32_t e = (uint32_t)gp[p] * 512u + (uint32_t)lane * 8u;
+            xoff[p] = e < (uint32_t)k * 4u ? e : 0x80000000u;
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p)
 #pragma unroll
             for (int b = 0; b < B; ++b)
-                xv[p][b] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                          x_rs[b], lane * 8, (uint32_t)gp[p] * 512, 0));
+                xv[p][b] = __builtin_bit_cast(float2,
+                                              __builtin_amdgcn_raw_buffer_load_b64(x_rs[b], xoff[p], 0, 0));
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const uint32_t soff = tile_off + (uint32_t)gp[p] * kChunk;
@@ -218,19 +238,22 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 const float x0 = xv[p][b].x, x1 = xv[p][b].y;
-                const uint32_t mb = row16_max(__float_as_uint(fmaxf(fabsf(x0), fabsf(x1))));
-                // 2^(e-1) <= max < 2^e with e = biased exponent - 126; s = 22 - e
-                shift[p][b] = 148 - (int)(mb >> 23);
-                // t = 1.5 * 2^23 + round(x * 2^s): bits(t) = 0x4B400000 + X (|X| <= 2^22)
-                const uint32_t t0 = __float_as_uint(__builtin_amdgcn_ldexpf(x0, shift[p][b]) + 12582912.0f);
-                const uint32_t t1 = __float_as_uint(__builtin_amdgcn_ldexpf(x1, shift[p][b]) + 12582912.0f);
-                seen[b] = max(seen[b], max(t0, t1));
-                // low three bytes of (X + 0x808080) ^ 0x808080: digits c, b, a
-                const uint32_t z0 = (t0 + (0x808080u - 0x4B400000u)) ^ 0x808080u;
-                const uint32_t z1 = (t1 + (0x808080u - 0x4B400000u)) ^ 0x808080u;
-                uint16_t* w16 = wr16 + (p * B + b) * 2 * 12 * 8;
+                const uint32_t mb = row16_max(max(__float_as_uint(x0) & 0x7FFFFFFFu,
+                                                  __float_as_uint(x1) & 0x7FFFFFFFu));
+                seen[b] = max(seen[b], mb);
+                // 2^(e-1) <= max < 2^e with e = biased exponent - 126; s = 30 - e
+                shift[p][b] = 156 - (int)(mb >> 23);
+                // X = round(x * 2^s), |X| < 2^30 (x * 2^s is an integer from 2^23 up);
+                // cvt_i32 also takes the inf / NaN of a non-finite block (its row's
+                // outputs become NaN below)
+                const int X0 = cvt_i32(__builtin_rintf(__builtin_amdgcn_ldexpf(x0, shift[p][b])));
+                const int X1 = cvt_i32(__builtin_rintf(__builtin_amdgcn_ldexpf(x1, shift[p][b])));
+                // bytes of (X + 0x80808080) ^ 0x80808080: the balanced digits, low first
+                const uint32_t z0 = ((uint32_t)X0 + 0x80808080u) ^ 0x80808080u;
+                const uint32_t z1 = ((uint32_t)X1 + 0x80808080u) ^ 0x80808080u;
+                uint16_t* w16 = wr16 + (p * B + b) * 2 * kHalfSlots * 8;
 #pragma unroll
-                for (int h = 0; h < 3; ++h)
+                for (int h = 0; h < kDigits; ++h)
                     w16[h * 8] = (uint16_t)__builtin_amdgcn_perm(z1, z0, (uint32_t)(h | ((4 + h) << 8) | 0x0C0C0000u));
             }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -257,15 +280,17 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                 const float d = g + p < g1 ? f16_bits_to_f32((uint16_t)sc[nw][p]) : 0.0f;
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
-                    const int base = (p * B + b) * 2 * 12;
-                    const uint4 v0 = my_lds[a_live ? base + a_slot : kZero];
-                    const uint4 v1 = my_lds[a_live ? base + 12 + a_slot : kZero];
+                    const int base = (p * B + b) * 2 * kHalfSlots;
+                    const uint4 v0 = my_lds[a_live ? base + ln : kZero];
+                    const uint4 v1 = my_lds[a_live ? base + kHalfSlots + ln : kZero];
                     i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w}, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
                     D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w}, b1, D, 0, 0, 0);
-                    // |D| <= 2^19 each: exact in fp32; the combination rounds once per step
-                    const float r = fmaf((float)D[2], 65536.0f, fmaf((float)D[1], 256.0f, (float)D[0]));
+                    // |D_h| <= 2^19: D_0 + 2^8 D_1 and D_2 + 2^8 D_3 are exact in int32;
+                    // their combination rounds once in fp32
+                    const int lo = D[0] + (int)((uint32_t)D[1] << 8), hi = D[2] + (int)((uint32_t)D[3] << 8);
+                    const float r = fmaf((float)hi, 65536.0f, (float)lo);
                     acc[nw][b] = fmaf(d, __builtin_amdgcn_ldexpf(r, -shift[p][b] - (kQ4 ? 4 : 0)), acc[nw][b]);
                 }
             }
@@ -277,7 +302,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
     // Any inf / NaN activation turns the outputs into NaN.
     bool bad[B];
 #pragma unroll
-    for (int b = 0; b < B; ++b) bad[b] = __ballot(seen[b] > 0x4B800000u) != 0;
+    for (int b = 0; b < B; ++b) bad[b] = __ballot(seen[b] >= 0x7F800000u) != 0;
 #pragma unroll
     for (int nw = 0; nw < kNW; ++nw)
 #pragma unroll
@@ -312,7 +337,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 
 template <bool kQ4, int B, int W, int P, int kKind>
 hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, hipStream_t s) {
-    static_assert(sizeof(uint4) * W * kSlots<B, P> <= 64 * 1024, "A-fragment LDS over budget");
+    // gfx950 gives a workgroup up to 160 KB of LDS; 4 batch rows x 8 waves take 66 KB
+    static_assert(sizeof(uint4) * W * kSlots<B, P> <= 80 * 1024, "A-fragment LDS over budget");
     const unsigned wgs = (unsigned)grp.tile_begin[kMaxGroup];
     hipLaunchKernelGGL((gemv_kernel<kQ4, B, W, P, kKind>), dim3(wgs), dim3(64 * W), 0, s, grp.chunks[0],
                        grp.chunks[1], x, grp.y[0], grp.n_rows[0], grp.tile_begin[1], (int)groups, (int)k, grp);

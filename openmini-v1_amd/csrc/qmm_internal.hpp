@@ -165,6 +165,9 @@ hipError_t launch_dequant_layout(int type, const uint8_t* gguf, size_t bytes, si
                                  hipStream_t s);
 
 hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+// Reads `bytes` (a multiple of 16) once; stores nothing in practice (a sentinel store to
+// sink[0] keeps the loads live).
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s);
 
 // ---- shared host helpers (qmm_api.hip) ----------------------------------------------
 

@@ -370,6 +370,26 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restric
         dst[i] = src[i];
 }
 
+// Read-only streaming yardstick: every 16-byte word of src is read once (kReadU loads in
+// flight per lane, workgroups of 512 lanes over consecutive 32 KB spans), folded into a
+// register, and nothing is stored unless a lane's fold equals a sentinel (which keeps
+// the loads live).  The single-launch floor a read-bound kernel of `bytes` meets.
+constexpr int kReadU = 4;
+__global__ __launch_bounds__(512) void stream_read_kernel(const uint4* __restrict__ src, int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
+    const int64_t base = (int64_t)blockIdx.x * (512 * kReadU) + threadIdx.x;
+    uint4 v[kReadU];
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) {
+        const int64_t i = base + (int64_t)u * 512;
+        v[u] = i < n16 ? src[i] : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < kReadU; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
 // quant_simd::convert_to_soa_layout's block arms (quant_simd.rs:3300-3397): output byte
 // o is byte (o & 1) of fp16 field f (scale; Q4_1 also min) of block b for o below
 // 2 * fields * blocks, else code position pos of block b, position-major.  A field is
@@ -504,6 +524,16 @@ hipError_t launch_stream_copy(void* dst, const void* src, size_t bytes, hipStrea
     if (blocks > 256 * 32) blocks = 256 * 32;
     hipLaunchKernelGGL(stream_copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
                        reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t s) {
+    const int64_t n16 = (int64_t)(bytes / 16);
+    if (n16 == 0) return hipSuccess;
+    const int64_t blocks = (n16 + 512 * kReadU - 1) / (512 * kReadU);
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(512), 0, s,
+                       reinterpret_cast<const uint4*>(src), n16, sink);
     return hipGetLastError();
 }
 

@@ -148,6 +148,13 @@ def stream_copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int, stream=None) 
     check(lib().openmini_qmm_stream_copy(dst.ptr, src.ptr, nbytes, stream))
 
 
+def stream_read(src: DeviceBuffer, nbytes: int, sink: DeviceBuffer, stream=None) -> None:
+    """The read-only streaming yardstick (openmini_qmm_stream_read): `nbytes` read once,
+    nothing written; the single-launch floor of a read-bound kernel of that size."""
+    assert nbytes <= src.nbytes and sink.nbytes >= 4
+    check(lib().openmini_qmm_stream_read(src.ptr, nbytes, sink.ptr, stream))
+
+
 def init(device: int = 0) -> None:
     check(lib().openmini_qmm_init(device))
 

@@ -172,3 +172,97 @@ def test_gemv_ragged_tiles(qmm, orc, qtype):
     for N, K in ((17, 32), (33, 160), (1000, 4000), (255, 4064)):
         case(qmm, orc, qtype, N, K, 1, seed=N + K)
         case(qmm, orc, qtype, N, K, 3, seed=N + K + 1)
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_gemv_ragged_k_reads_stop_at_k(qmm, orc, qtype):
+    """K = 160 leaves the last 4-block group one block long: the kernel must read no
+    activation past a row's K elements.  Row 1 starts with a NaN right after row 0's
+    last element, and row 0 must still match the oracle."""
+    N, K = 48, 160
+    blocks = synth.weight_blocks(qtype, N, K, seed=67)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(68, (2, K), 1.0)
+    x[1, 0] = np.nan
+    y = run_gemv(qmm, w, x)
+    assert_parity(y[:1], orc.linear_f64(qtype, blocks, N, K, x[:1]), TOL, "row 0")
+    assert not np.any(np.isfinite(y[1]))
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("B", [1, 3, 5])
+def test_gemv_x_in_nan_tailed_buffer(qmm, orc, qtype, B):
+    """x at the start of a larger allocation whose tail is NaN (K = 4000: the last
+    group holds one block): nothing past x[B, K] is read, by the single-row kernel
+    (B = 1, 3) or the batched one (B = 5)."""
+    N, K = 40, 4000
+    blocks = synth.weight_blocks(qtype, N, K, seed=69 + B)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(70 + B, (B, K), 1.0)
+    buf = np.full(B * K + 1024, np.nan, np.float32)
+    buf[:B * K] = x.ravel()
+    dx = qmm.DeviceBuffer.from_numpy(buf)
+    dy = qmm.DeviceBuffer(B * N * 4)
+    w.gemv(dx, dy, B)
+    assert_parity(dy.download(np.float32, (B, N)), orc.linear_f64(qtype, blocks, N, K, x), TOL, "tail")
+
+
+def _zero_column(qtype, blocks, N, K, c):
+    """The GGUF blocks with element c of every row set to the code of 0.0."""
+    bpb = 18 if qtype == Q4_0 else 34
+    b = blocks.copy().reshape(N, K // 32, bpb)
+    j = c % 32
+    if qtype == Q4_0:  # code 8; element 2i in the high nibble of byte i
+        byte = 2 + j // 2
+        b[:, c // 32, byte] = ((b[:, c // 32, byte] & 0x0F) | 0x80) if j % 2 == 0 \
+            else ((b[:, c // 32, byte] & 0xF0) | 0x08)
+    else:
+        b[:, c // 32, 2 + j] = 0
+    return b.ravel()
+
+
+def _adversarial_rows(w_f32, K, seed):
+    """Activation rows that stress a per-block representation of x:
+    0  a x3e4 outlier on a feature every weight row ignores (its weights are 0), so
+       the block's other 31 elements carry the output at 1e-4 of the block maximum;
+    1  mixed exponents: N(0, 1) * 2^u, u uniform in [-20, 20], per element;
+    2  near-cancelling: projected so outputs 0..7 are ~0 (error is all absolute);
+    3  a x3e4 outlier on a feature the weights use."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((4, K)).astype(np.float32)
+    x[0, 5] = np.float32(3e4)
+    x[1] = (x[1] * np.exp2(rng.integers(-20, 21, K))).astype(np.float32)
+    xx = x[2].astype(np.float64)
+    for r in range(8):
+        wr = w_f32[r].astype(np.float64)
+        xx = xx - (xx @ wr) / (wr @ wr) * wr
+    x[2] = xx.astype(np.float32)
+    x[3, 100] = np.float32(3e4)
+    return x
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("B", [4, 8])
+def test_gemv_error_within_fp32_path(qmm, orc, qtype, B):
+    """The activation arithmetic is not narrower than the reference's f32 path: on
+    adversarial rows, the largest error of each output row against the fp64 oracle is
+    at most 4x that of the f32 GEMV over the dequantized weights (the reference's
+    per-token path, oracle.cpu_asrun_linear).  B = 4 runs the single-row kernel
+    (30-bit block-floating activations), B = 8 the batched one (fp16 hi / lo split)."""
+    N, K = 512, 4096
+    blocks = _zero_column(qtype, synth.weight_blocks(qtype, N, K, seed=0xAD0 + qtype), N, K, 5)
+    w_f32 = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
+    assert np.all(w_f32[:, 5] == 0.0)
+    x = _adversarial_rows(w_f32, K, 0xAD1)
+    if B > 4:
+        x = np.concatenate([x, synth.normal(0xAD2, (B - 4, K), 1.0)])
+    wq = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y = run_gemv(qmm, wq, x)
+    ref = orc.linear_f64(qtype, blocks, N, K, x)
+    y32 = orc.cpu_asrun_linear(w_f32, x, None, False)
+    for r in range(B):
+        e_gpu = float(np.max(np.abs(y[r] - ref[r])))
+        e_f32 = float(np.max(np.abs(y32[r] - ref[r])))
+        print(f"row {r}: gpu {e_gpu:.3e} f32 path {e_f32:.3e}")
+        assert e_gpu <= 4.0 * e_f32, (r, e_gpu, e_f32)
+        assert_parity(y[r:r + 1], ref[r:r + 1], TOL, f"row {r}")
