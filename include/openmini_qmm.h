@@ -192,6 +192,18 @@ int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,
                              int64_t m);
 
+/* openmini_qmm_linear_host without any allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  x and y are staged through a
+ * fixed 16 MiB device array that the library holds on every device it runs on until
+ * the process ends (x first, y from the next 256-byte boundary): m * (K + N) * 4
+ * bytes must fit in 16 MiB - 256, else INVALID_PARAM naming the row limit.  Same
+ * kernels and results as openmini_qmm_linear_host, synchronous on the null stream.
+ * All calls on one device share the array, so calls that overlap on one device race;
+ * nothing in it needs clearing (x and y are written whole by every call). */
+int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const float* x, float* y,
+                                     int64_t m);
+
 /* ---- dequantization (GpuQuantOps, src/model/inference/quant_simd.rs:2944-2986) ----- */
 
 /* Dequantizes an uploaded weight to f32 W[N, K] (row-major) in device memory.

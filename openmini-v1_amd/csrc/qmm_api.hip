@@ -178,6 +178,33 @@ int check_weight(const openmini_qweight* h) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ---- device staging of openmini_qmm_linear_host_noalloc ----------------------------
+// x, then y at the next 256-byte boundary, in one file-scope array that every device
+// the library runs on holds until the process ends.  Its name is a host-side stand-in:
+// the device address of each device's copy comes from hipGetSymbolAddress, resolved
+// once per device with that device current and kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[64];  // per device ordinal; nullptr until resolved
+
+// The current device's address of `scratch` (dev = the current device).
+int scratch_on_device(int dev, uint8_t** out) {
+    hipError_t e = hipSuccess;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            void* p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e == hipSuccess) g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+        }
+        *out = g_scratch_ptr[dev];
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    return OPENMINI_QMM_OK;
+}
+
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 }  // namespace
@@ -253,6 +280,9 @@ int openmini_qmm_init(int device) {
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "device %d out of range (count %d)", device, count);
     HIP_TRY(hipSetDevice(device), "hipSetDevice");
     int rc = ensure_device(nullptr);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    uint8_t* staging = nullptr;  // resolve the no-allocation staging while `device` is current
+    rc = scratch_on_device(device, &staging);
     if (rc != OPENMINI_QMM_OK) return rc;
     return ok();
 }
@@ -479,6 +509,32 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
     (void)hipFree(dx);
     (void)hipFree(dy);
     if (e != hipSuccess) return hip_fail(e, "linear_host");
+    return ok();
+}
+
+int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const float* x, float* y, int64_t m) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!x || !y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
+    if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
+    const qmm::Weight& w = weight->w;
+    const size_t row_bytes = (size_t)(w.k + w.n) * sizeof(float);  // one row of x and of y
+    const size_t limit = kScratchBytes - 256;                        // y starts 256-aligned
+    if ((uint64_t)m > limit / row_bytes)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM,
+                    "linear_host_noalloc: m=%lld rows of x[K=%lld] and y[N=%lld] need more than the %zu-byte "
+                    "staging (at most %zu rows for this weight)",
+                    (long long)m, (long long)w.k, (long long)w.n, kScratchBytes, limit / row_bytes);
+    uint8_t* base = nullptr;
+    rc = scratch_on_device(w.device, &base);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
+    float* dx = reinterpret_cast<float*>(base);
+    float* dy = reinterpret_cast<float*>(base + round_up(xb, 256));
+    hipError_t e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = qmm::launch_gemv_rows(w, nullptr, dx, dy, m, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(y, dy, yb, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "linear_host_noalloc");
     return ok();
 }
 

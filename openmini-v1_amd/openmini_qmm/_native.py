@@ -90,6 +90,7 @@ SIGNATURES = {
     "openmini_qmm_ffn_gate_up": (_i, [_p, _p, _p, _p, _i64, _p]),
     "openmini_qmm_ffn_gate_up_bf16": (_i, [_p, _p, _p, _p, _i64, _p]),
     "openmini_qmm_linear_host": (_i, [_p, _p, _p, _i64]),
+    "openmini_qmm_linear_host_noalloc": (_i, [_p, _p, _p, _i64]),
     "openmini_qmm_dequant_weight": (_i, [_p, _p, _p]),
     "openmini_qmm_dequantize_device": (_i, [_i, _p, _sz, _sz, _p, _p, ctypes.POINTER(_sz)]),
     "openmini_qmm_dequantize": (_i, [_i, _p, _sz, _sz, _p, ctypes.POINTER(_sz)]),
