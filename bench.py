@@ -35,7 +35,8 @@ sys.path.insert(0, os.path.join(ROOT, "openmini-v1_amd"))
 METRIC = "Q4_0 GEMV HBM GB/s (% of peak) at 4096x11008 b=1; Q8_0 GEMM TFLOP/s M=512"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-Q4_0, Q8_0 = 2, 7
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 12, 14
+TYPE_NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
 MALL_DEFEAT_BYTES = 1 << 30
 
 
@@ -80,8 +81,9 @@ def time_steps(launch, steps: int, stream, hipr) -> float:
 
 def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed=0x5EED0001):
     from openmini_qmm import synth
-    blocks = synth.weight_blocks(qtype, N, K, seed=seed)
-    wbytes = blocks.size
+    blocks = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
+              else synth.weight_blocks(qtype, N, K, seed=seed))
+    wbytes = blocks.size  # GGUF bytes: the algorithmic weight bytes
     copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
     log(f"gemv type={qtype} N={N} K={K} B={batch}: {copies} weight copies x {wbytes} B")
     ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
@@ -498,6 +500,18 @@ def main(argv=None) -> int:
                            "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
                            "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})
             log(f"decode {shapes[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
+    kquant = []
+    if not args.no_shapes:
+        # decode GEMV on K-quant weights (Llama-7B up / down shapes, batch 1)
+        for qtype, n, k, seed in ((Q4_K, 11008, 4096, 0x5EED0071), (Q4_K, 4096, 11008, 0x5EED0072),
+                                  (Q6_K, 11008, 4096, 0x5EED0073), (Q6_K, 4096, 11008, 0x5EED0074)):
+            r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
+                           qtype=qtype, batch=1, seed=seed)
+            kquant.append({"workload": f"{TYPE_NAME[qtype]}_gemv_n{n}_k{k}_b1", "unit": "GB/s",
+                           "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                           "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
+                           "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})
+            log(f"decode {kquant[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
     wpath = None
     if not args.no_weight_path:
         wpath = bench_weight_path(qmm, hipr, stream, max(20, args.steps // 4), max(3, args.warmup // 4))
@@ -564,6 +578,8 @@ def main(argv=None) -> int:
         out["batched_decode"] = batched
     if shapes:
         out["decode_shapes"] = shapes
+    if kquant:
+        out["kquant_decode"] = kquant
     if wpath:
         out["weight_path"] = wpath
     if layer:

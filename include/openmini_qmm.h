@@ -54,8 +54,9 @@ typedef enum {
     OPENMINI_QMM_ERR_NOT_FOUND = -12     /* "Tensor not found" / missing metadata key */
 } openmini_qmm_status_t;
 
-/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload, GEMV and
- * GEMM take Q4_0 and Q8_0; the dequantization entry points take every id listed. */
+/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload and the
+ * decode GEMV take Q4_0, Q8_0, Q4_K and Q6_K; the prefill GEMM takes Q4_0 and Q8_0; the
+ * dequantization entry points take every id listed. */
 typedef enum {
     OPENMINI_QMM_F32 = 0,
     OPENMINI_QMM_F16 = 1,
@@ -77,9 +78,9 @@ typedef struct {
     int32_t type;            /* openmini_qmm_type_t */
     int32_t device;          /* HIP device ordinal holding the weight */
     int64_t n_rows;          /* N: output features */
-    int64_t k_cols;          /* K: input features, a multiple of 32 */
-    int64_t blocks_per_row;  /* K / 32 */
-    size_t gguf_bytes;       /* N * K / 32 * bytes_per_block (GGUF data_size) */
+    int64_t k_cols;          /* K: input features, a multiple of 32 (256 for Q4_K / Q6_K) */
+    int64_t blocks_per_row;  /* K / 32 (32-element sub-blocks for Q4_K / Q6_K) */
+    size_t gguf_bytes;       /* GGUF data_size: N * K / 32 * 18 | 34, N * K / 256 * 144 | 210 */
     size_t device_bytes;     /* HBM held by the handle */
 } openmini_qmm_weight_info_t;
 
@@ -129,8 +130,11 @@ size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
  * (gguf.rs:2062-2110) -> quant::dequantize (quant.rs:56).  Takes the tensor's raw
  * GGUF blocks (row n = k_cols/32 consecutive blocks, ggml ne0 = K), keeps them
  * quantized and repacks them on the GPU for its access pattern.
- * Errors: INVALID_PARAM (k_cols % 32, sizes <= 0), UNSUPPORTED (type),
- * INSUFFICIENT_DATA (gguf_bytes < required). */
+ * Types: Q4_0 and Q8_0 (GEMV and GEMM), Q4_K and Q6_K (GEMV; with the reference's own
+ * reading of those blocks, quant.rs:338-410 and :515-600, whose values are exact
+ * products of an integer code and an fp32 sub-block factor).
+ * Errors: INVALID_PARAM (k_cols % 32, or % 256 for Q4_K / Q6_K; sizes <= 0),
+ * UNSUPPORTED (type), INSUFFICIENT_DATA (gguf_bytes < required). */
 int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes,
                         int64_t n_rows, int64_t k_cols, openmini_qweight_t** out_weight);
 
@@ -152,14 +156,15 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
 /* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
  * Any batch >= 1.  Up to 4 rows: the single-row-tuned kernel (one launch per 4
  * rows); 5 or more: the batched kernel, one pass over W per 16 rows, in which a
- * row's result does not depend on the other rows of the call.
+ * row's result does not depend on the other rows of the call (Q4_K / Q6_K weights
+ * use the single-row kernel for every batch, one launch per 4 rows).
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);
 
 /* Prefill GEMM: y[m, N] = x[m, K] . W^T with bf16 activations (raw bf16 bits),
  * fp32 output, on bf16 MFMA with exact integer codes and fp32 per-block scales.
- * d_x must be 16-byte aligned. */
+ * Q4_0 and Q8_0 weights (UNSUPPORTED for Q4_K / Q6_K).  d_x must be 16-byte aligned. */
 int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
                            int64_t m, void* stream);
 
@@ -206,8 +211,10 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
 
 /* ---- dequantization (GpuQuantOps, src/model/inference/quant_simd.rs:2944-2986) ----- */
 
-/* Dequantizes an uploaded weight to f32 W[N, K] (row-major) in device memory.
- * Bit-identical to quant::dequantize of the original GGUF bytes. */
+/* Dequantizes an uploaded Q4_0 / Q8_0 weight to f32 W[N, K] (row-major) in device memory
+ * (d_out 16-byte aligned).  Bit-identical to quant::dequantize of the original GGUF bytes.
+ * UNSUPPORTED for Q4_K / Q6_K handles: their GGUF bytes dequantize through
+ * openmini_qmm_dequantize_any_device. */
 int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, void* stream);
 
 /* quant_simd::safe_dequantize semantics (quant_simd.rs:150-302) on raw GGUF bytes in
@@ -323,7 +330,7 @@ int openmini_qmm_gguf_get_string(const openmini_qmm_gguf_t* gguf, const char* ke
 
 /* QuantizedWeightLoader::load_tensor (quant_loader.rs:66-92) without dequantization: the
  * 2-D tensor [ne0 = K, ne1 = N] becomes the weight W[N, K] (row n = K consecutive
- * elements, the semantic layout linear() multiplies by); Q4_0 / Q8_0 only (UNSUPPORTED
+ * elements, the semantic layout linear() multiplies by); Q4_0 / Q8_0 / Q4_K / Q6_K (UNSUPPORTED
  * otherwise).  Copy and repack run on `stream`, synchronised before returning. */
 int openmini_qmm_gguf_upload_weight(const openmini_qmm_gguf_t* gguf, const char* name, void* stream,
                                     openmini_qweight_t** out_weight);

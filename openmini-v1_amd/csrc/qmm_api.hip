@@ -65,10 +65,15 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
-// Weight layouts (upload, GEMV, GEMM).
-bool type_supported(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
+// Weight layouts of the upload and the decode GEMV; the GEMM takes Q4_0 and Q8_0.
+bool type_supported(int type) {
+    return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0 || qmm::is_kquant(type);
+}
+bool gemm_type(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
 // quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
-bool safe_type(int type) { return type_supported(type) || type == OPENMINI_QMM_Q4_1; }
+bool safe_type(int type) {
+    return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0 || type == OPENMINI_QMM_Q4_1;
+}
 // ceil(n / block_size) * bytes_per_block (gguf.rs:431-438); 0 for unknown types.
 // Element counts above 2^48 (1 PB of f32) are rejected, so every size computed
 // from one (bytes of any layout, n * sizeof(float)) fits in 64 bits.
@@ -114,13 +119,14 @@ size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_cols) {
     if (!type_supported(type))
-        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d (Q4_0=2, Q8_0=7)", type);
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d (Q4_0=2, Q8_0=7, Q4_K=12, Q6_K=14)",
+                    type);
     if (n_rows <= 0 || k_cols <= 0)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "invalid shape [%lld, %lld]", (long long)n_rows,
                     (long long)k_cols);
-    if (k_cols % qmm::kQK != 0)
-        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "k_cols=%lld is not a multiple of 32",
-                    (long long)k_cols);
+    const int be = qmm::weight_block_elems(type);  // 32, or 256 for the K-quant super-blocks
+    if (k_cols % be != 0)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "k_cols=%lld is not a multiple of %d", (long long)k_cols, be);
     if (n_rows > INT32_MAX || k_cols / qmm::kQK > INT32_MAX / 64)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld] too large", (long long)n_rows,
                     (long long)k_cols);
@@ -133,7 +139,7 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
     if (chunked >= ((size_t)1 << 32))
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld]: %zu weight bytes exceed 4 GiB",
                     (long long)n_rows, (long long)k_cols, chunked);
-    const size_t need = (size_t)n_rows * (size_t)(k_cols / qmm::kQK) * qmm::bytes_per_block(type);
+    const size_t need = (size_t)n_rows * (size_t)(k_cols / be) * qmm::bytes_per_block(type);
     if (gguf_bytes < need)
         return fail(OPENMINI_QMM_ERR_INSUFFICIENT_DATA,
                     "InsufficientData: expected %zu bytes, actual %zu", need, gguf_bytes);
@@ -222,7 +228,7 @@ int upload_from_host(int type, const void* host_blocks, size_t bytes, int64_t n_
     int dev = 0;
     rc = ensure_device(&dev);
     if (rc != OPENMINI_QMM_OK) return rc;
-    const size_t need = (size_t)n_rows * (size_t)(k_cols / kQK) * bytes_per_block(type);
+    const size_t need = (size_t)n_rows * (size_t)(k_cols / weight_block_elems(type)) * bytes_per_block(type);
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, need);
     if (e != hipSuccess)
@@ -383,7 +389,7 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight, openmini_qmm_weig
     info->n_rows = w.n;
     info->k_cols = w.k;
     info->blocks_per_row = w.nb;
-    info->gguf_bytes = (size_t)w.n * (size_t)w.nb * qmm::bytes_per_block(w.type);
+    info->gguf_bytes = (size_t)w.n * (size_t)(w.k / qmm::weight_block_elems(w.type)) * qmm::bytes_per_block(w.type);
     info->device_bytes = w.device_bytes;
     return ok();
 }
@@ -407,6 +413,9 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    if (!gemm_type(weight->w.type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "the prefill GEMM takes Q4_0 and Q8_0 weights, not type %d",
+                    weight->w.type);
     hipError_t e = qmm::launch_gemm_bf16(weight->w, d_x, d_y, m, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return ok();
@@ -482,6 +491,9 @@ int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini
     if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    if (!gemm_type(gate->w.type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "the prefill GEMM takes Q4_0 and Q8_0 weights, not type %d",
+                    gate->w.type);
     hipError_t e = qmm::launch_gemm_bf16(gate->w, d_x, d_h, m, as_stream(stream), false);
     if (e == hipSuccess) e = qmm::launch_gemm_bf16(up->w, d_x, d_h, m, as_stream(stream), true);
     if (e != hipSuccess) return hip_fail(e, "ffn_gate_up_bf16 launch");
@@ -543,6 +555,9 @@ int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, 
     if (rc != OPENMINI_QMM_OK) return rc;
     if (!d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out");
     if (!aligned16(d_out)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "out must be 16-byte aligned");
+    if (!gemm_type(weight->w.type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
+                    "dequant_weight takes Q4_0 and Q8_0 weights (K-quant bytes: openmini_qmm_dequantize_any_device)");
     hipError_t e = qmm::launch_dequant_weight(weight->w, d_out, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "dequant launch");
     return ok();

@@ -86,6 +86,14 @@ __device__ __forceinline__ int cvt_i32(float v) {
     return r;
 }
 
+// One block's digit dot products (D_h: register h) -> their weighted sum
+// D_0 + 2^8 D_1 + 2^16 (D_2 + 2^8 D_3): |D_h| <= 2^19, so each half is exact in int32
+// and the combination rounds once in fp32.
+__device__ __forceinline__ float digit_sum(const i32x4& D) {
+    const int lo = D[0] + (int)((uint32_t)D[1] << 8), hi = D[2] + (int)((uint32_t)D[3] << 8);
+    return fmaf((float)hi, 65536.0f, (float)lo);
+}
+
 // Raw buffer resource (gfx9 descriptor): out-of-range loads return zero, offsets are
 // 32-bit with the uniform part in an SGPR.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -115,16 +123,33 @@ constexpr int kSlots = P * B * 2 * 4 * kDigits + 1;
 // (gate, up) pair run on the same tiles.
 constexpr int kOne = 0, kGroup = 1, kPair = 2;
 
-template <bool kQ4, int B, int W, int P, int kKind>
+// Chunk geometry of a weight format (kFmt = its GGUF type id; qmm_internal.hpp):
+// bytes of a slot's codes, where the per-slot scale and the per-row d live, and the
+// power of two the int8 code bytes carry (Q4_0 / Q4_K codes are 16 (q - 8), Q6_K 4 q).
+template <int kFmt>
+struct Fmt {
+    static constexpr bool kNib = kFmt == OPENMINI_QMM_Q4_0 || kFmt == OPENMINI_QMM_Q4_K;  // 16 B of nibbles
+    static constexpr bool kQ6 = kFmt == OPENMINI_QMM_Q6_K;
+    static constexpr bool kKQ = kFmt == OPENMINI_QMM_Q4_K || kQ6;                        // K-quant
+    static constexpr int kCB = kNib ? 16 : kQ6 ? 24 : 32;
+    static constexpr int kCodeBytes = kTileEntries * kCB;
+    static constexpr int kChunk = kFmt == OPENMINI_QMM_Q4_K ? kQ4KChunk
+                                  : kQ6                     ? kQ6KChunk
+                                                            : chunk_bytes_for(kFmt == OPENMINI_QMM_Q4_0);
+    static constexpr int kDOff = kCodeBytes + (kQ6 ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
+    static constexpr int kCodeShift = kNib ? 4 : kQ6 ? 2 : 0;
+};
+
+template <int kFmt, int B, int W, int P, int kKind>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict__ w0,
                                                       const uint8_t* __restrict__ w1,
                                                       const float* __restrict__ x, float* __restrict__ y0,
                                                       int n_rows0, int tiles0, int groups, int k,
                                                       const GemvGroup grp) {
+    using F = Fmt<kFmt>;
     constexpr int kNW = kKind == kPair ? 2 : 1;  // weights per tile
-    constexpr int kCB = kQ4 ? 16 : 32;
-    constexpr int kCodeBytes = kTileEntries * kCB;
-    constexpr int kChunk = chunk_bytes_for(kQ4);
+    constexpr int kCodeBytes = F::kCodeBytes;
+    constexpr int kChunk = F::kChunk;
     constexpr int kS = kSlots<B, P>;
     constexpr int kZero = kS - 1;
     __shared__ uint4 a_lds[W][kS];
@@ -199,8 +224,10 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
         for (int p = 0; p < P; ++p) gp[p] = min(g + p, g1 - 1);
         float2 xv[P][B];
-        uint4 c[kNW][P][kQ4 ? 1 : 2];
-        uint32_t sc[kNW][P];
+        uint4 c[kNW][P][F::kNib ? 1 : 2];
+        uint2 hb[kNW][P];      // Q6_K: the slot's 8 bytes of top code bits
+        uint32_t sc[kNW][P];   // the slot's scale: fp16 bits (Q4_0 / Q8_0), u8 (Q4_K), 2 x int8 (Q6_K)
+        uint32_t dk[kNW][P];   // K-quant: the row's fp16 d
         // activations first: L2 hits that land before the weights do.  The whole offset
         // goes in the VGPR operand: the raw-buffer range check covers the VGPR offset
         // but not the SGPR one, so elements past k (a last group of fewer than 4
@@ -222,12 +249,20 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
             const uint32_t soff = tile_off + (uint32_t)gp[p] * kChunk;
 #pragma unroll
             for (int nw = 0; nw < kNW; ++nw) {
-                c[nw][p][0] = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * kCB, soff, 0));
-                if constexpr (!kQ4)
+                c[nw][p][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            w_rs[nw], lane * (F::kQ6 ? 16 : F::kCB), soff, 0));
+                if constexpr (kFmt == OPENMINI_QMM_Q8_0)
                     c[nw][p][1] = __builtin_bit_cast(
-                        uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * kCB + 16, soff, 0));
-                sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kCodeBytes + lane * 2, soff, 0);
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * 32 + 16, soff, 0));
+                if constexpr (F::kQ6)
+                    hb[nw][p] = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(w_rs[nw], kTileEntries * 16 + lane * 8, soff, 0));
+                if constexpr (kFmt == OPENMINI_QMM_Q4_K)
+                    sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b8(w_rs[nw], kCodeBytes + lane, soff, 0);
+                else
+                    sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kCodeBytes + lane * 2, soff, 0);
+                if constexpr (F::kKQ)
+                    dk[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], F::kDOff + ln * 2, soff, 0);
             }
         }
 
@@ -265,33 +300,65 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
 #pragma unroll
             for (int nw = 0; nw < kNW; ++nw) {
                 i32x4 b0, b1;
-                if constexpr (kQ4) {
+                if constexpr (F::kNib) {
                     // 16 * (q - 8) as int8 bytes, elements in order
                     const uint4 w = c[nw][p][0];
                     b0 = i32x4{(int)((w.x << 4) & 0xF0F0F0F0u), (int)(w.x & 0xF0F0F0F0u),
                                (int)((w.y << 4) & 0xF0F0F0F0u), (int)(w.y & 0xF0F0F0F0u)};
                     b1 = i32x4{(int)((w.z << 4) & 0xF0F0F0F0u), (int)(w.z & 0xF0F0F0F0u),
                                (int)((w.w << 4) & 0xF0F0F0F0u), (int)(w.w & 0xF0F0F0F0u)};
+                } else if constexpr (F::kQ6) {
+                    // 4 q as int8 bytes: low 4 bits of the 6-bit code at bits 2..5, its top
+                    // 2 bits at 6..7 (field f of top-bit word m: element 16 m + 4 f + i)
+                    const uint4 w = c[nw][p][0];
+                    const uint2 h = hb[nw][p];
+                    auto lo = [](uint32_t wj, uint32_t hm, int sh) {
+                        return (int)(((wj << 2) & 0x3C3C3C3Cu) | ((hm << sh) & 0xC0C0C0C0u));
+                    };
+                    auto hi = [](uint32_t wj, uint32_t hm, int sh) {
+                        return (int)(((wj >> 2) & 0x3C3C3C3Cu) | ((hm << sh) & 0xC0C0C0C0u));
+                    };
+                    b0 = i32x4{lo(w.x, h.x, 6), hi(w.x, h.x, 4), lo(w.y, h.x, 2), hi(w.y, h.x, 0)};
+                    b1 = i32x4{lo(w.z, h.y, 6), hi(w.z, h.y, 4), lo(w.w, h.y, 2), hi(w.w, h.y, 0)};
                 } else {
                     const uint4 w0 = c[nw][p][0], w1 = c[nw][p][1];
                     b0 = i32x4{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w};
                     b1 = i32x4{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
                 }
-                const float d = g + p < g1 ? f16_bits_to_f32((uint16_t)sc[nw][p]) : 0.0f;
+                // the slot's fp32 factor(s), exact: fp16 scale; Q4_K d * scale; Q6_K d * scale
+                // of each 16-element half.  Groups past the slice end get 0.
+                const bool live = g + p < g1;
+                float d0, d1 = 0.0f;
+                if constexpr (kFmt == OPENMINI_QMM_Q4_K) {
+                    d0 = f16_bits_to_f32((uint16_t)dk[nw][p]) * (float)sc[nw][p];
+                } else if constexpr (F::kQ6) {
+                    const float dd = f16_bits_to_f32((uint16_t)dk[nw][p]);
+                    d0 = dd * (float)(int8_t)(sc[nw][p] & 0xFFu);
+                    d1 = dd * (float)(int8_t)((sc[nw][p] >> 8) & 0xFFu);
+                    d1 = live ? d1 : 0.0f;
+                } else {
+                    d0 = f16_bits_to_f32((uint16_t)sc[nw][p]);
+                }
+                d0 = live ? d0 : 0.0f;
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
                     const int base = (p * B + b) * 2 * kHalfSlots;
                     const uint4 v0 = my_lds[a_live ? base + ln : kZero];
                     const uint4 v1 = my_lds[a_live ? base + kHalfSlots + ln : kZero];
-                    i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w}, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
-                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w}, b1, D, 0, 0, 0);
-                    // |D_h| <= 2^19: D_0 + 2^8 D_1 and D_2 + 2^8 D_3 are exact in int32;
-                    // their combination rounds once in fp32
-                    const int lo = D[0] + (int)((uint32_t)D[1] << 8), hi = D[2] + (int)((uint32_t)D[3] << 8);
-                    const float r = fmaf((float)hi, 65536.0f, (float)lo);
-                    acc[nw][b] = fmaf(d, __builtin_amdgcn_ldexpf(r, -shift[p][b] - (kQ4 ? 4 : 0)), acc[nw][b]);
+                    const i32x4 A0 = i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w};
+                    const i32x4 A1 = i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+                    const int sh = -shift[p][b] - F::kCodeShift;
+                    if constexpr (F::kQ6) {
+                        // the halves carry different scales: one MFMA each, not chained
+                        const i32x4 D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        const i32x4 D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        acc[nw][b] = fmaf(d0, __builtin_amdgcn_ldexpf(digit_sum(D0), sh), acc[nw][b]);
+                        acc[nw][b] = fmaf(d1, __builtin_amdgcn_ldexpf(digit_sum(D1), sh), acc[nw][b]);
+                    } else {
+                        i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, D, 0, 0, 0);
+                        acc[nw][b] = fmaf(d0, __builtin_amdgcn_ldexpf(digit_sum(D), sh), acc[nw][b]);
+                    }
                 }
             }
         // The next phase rewrites this wave's slots; a wave's LDS operations complete
@@ -335,12 +402,12 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
     }
 }
 
-template <bool kQ4, int B, int W, int P, int kKind>
+template <int kFmt, int B, int W, int P, int kKind>
 hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, hipStream_t s) {
     // gfx950 gives a workgroup up to 160 KB of LDS; 4 batch rows x 8 waves take 66 KB
     static_assert(sizeof(uint4) * W * kSlots<B, P> <= 80 * 1024, "A-fragment LDS over budget");
     const unsigned wgs = (unsigned)grp.tile_begin[kMaxGroup];
-    hipLaunchKernelGGL((gemv_kernel<kQ4, B, W, P, kKind>), dim3(wgs), dim3(64 * W), 0, s, grp.chunks[0],
+    hipLaunchKernelGGL((gemv_kernel<kFmt, B, W, P, kKind>), dim3(wgs), dim3(64 * W), 0, s, grp.chunks[0],
                        grp.chunks[1], x, grp.y[0], grp.n_rows[0], grp.tile_begin[1], (int)groups, (int)k, grp);
     return hipGetLastError();
 }
@@ -350,29 +417,37 @@ hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, 
 // e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  More batch rows: at most 8 (LDS and
 // registers per wave grow with the batch).  Short K: the most slices that keep 4
 // groups per wave.
-template <bool kQ4, int B, int kKind>
+template <int kFmt, int B, int kKind>
 hipError_t run_w(const GemvGroup& grp, int64_t g, int64_t k, const float* x, hipStream_t s) {
     if (g >= 32) {
         if constexpr (B == 1) {
             const int64_t pad16 = (g + 63) / 64 * 64 - g, pad8 = (g + 31) / 32 * 32 - g;
-            if (pad16 <= pad8) return run<kQ4, B, 16, 4, kKind>(grp, g, k, x, s);
+            if (pad16 <= pad8) return run<kFmt, B, 16, 4, kKind>(grp, g, k, x, s);
         }
-        return run<kQ4, B, 8, 4, kKind>(grp, g, k, x, s);
+        return run<kFmt, B, 8, 4, kKind>(grp, g, k, x, s);
     }
-    if (g >= 16) return run<kQ4, B, 4, 4, kKind>(grp, g, k, x, s);
-    if (g >= 8) return run<kQ4, B, 2, 4, kKind>(grp, g, k, x, s);
-    return run<kQ4, B, 1, 4, kKind>(grp, g, k, x, s);
+    if (g >= 16) return run<kFmt, B, 4, 4, kKind>(grp, g, k, x, s);
+    if (g >= 8) return run<kFmt, B, 2, 4, kKind>(grp, g, k, x, s);
+    return run<kFmt, B, 1, 4, kKind>(grp, g, k, x, s);
 }
 
-template <bool kQ4, int kKind>
+template <int kFmt, int kKind>
 hipError_t dispatch(const GemvGroup& grp, int64_t g, int64_t k, const float* x, int batch, hipStream_t s) {
     switch (batch) {
-    case 1: return run_w<kQ4, 1, kKind>(grp, g, k, x, s);
-    case 2: return run_w<kQ4, 2, kKind>(grp, g, k, x, s);
-    case 3: return run_w<kQ4, 3, kKind>(grp, g, k, x, s);
-    case 4: return run_w<kQ4, 4, kKind>(grp, g, k, x, s);
+    case 1: return run_w<kFmt, 1, kKind>(grp, g, k, x, s);
+    case 2: return run_w<kFmt, 2, kKind>(grp, g, k, x, s);
+    case 3: return run_w<kFmt, 3, kKind>(grp, g, k, x, s);
+    case 4: return run_w<kFmt, 4, kKind>(grp, g, k, x, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+template <int kFmt>
+hipError_t dispatch_kind(const GemvGroup& grp, const Weight& w0, const float* x, int batch, int count, bool swiglu,
+                         hipStream_t s) {
+    if (swiglu) return dispatch<kFmt, kPair>(grp, w0.groups, w0.k, x, batch, s);
+    if (count > 1) return dispatch<kFmt, kGroup>(grp, w0.groups, w0.k, x, batch, s);
+    return dispatch<kFmt, kOne>(grp, w0.groups, w0.k, x, batch, s);
 }
 
 }  // namespace
@@ -395,15 +470,13 @@ hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int coun
     for (int i = owners; i <= kMaxGroup; ++i) grp.tile_begin[i] = (int)tiles;
     if (tiles > INT32_MAX) return hipErrorInvalidValue;
     const Weight& w0 = *ws[0];
-    const bool q4 = w0.type == OPENMINI_QMM_Q4_0;
-    if (swiglu)
-        return q4 ? dispatch<true, kPair>(grp, w0.groups, w0.k, x, batch, s)
-                  : dispatch<false, kPair>(grp, w0.groups, w0.k, x, batch, s);
-    if (count > 1)
-        return q4 ? dispatch<true, kGroup>(grp, w0.groups, w0.k, x, batch, s)
-                  : dispatch<false, kGroup>(grp, w0.groups, w0.k, x, batch, s);
-    return q4 ? dispatch<true, kOne>(grp, w0.groups, w0.k, x, batch, s)
-              : dispatch<false, kOne>(grp, w0.groups, w0.k, x, batch, s);
+    switch (w0.type) {
+    case OPENMINI_QMM_Q4_0: return dispatch_kind<OPENMINI_QMM_Q4_0>(grp, w0, x, batch, count, swiglu, s);
+    case OPENMINI_QMM_Q8_0: return dispatch_kind<OPENMINI_QMM_Q8_0>(grp, w0, x, batch, count, swiglu, s);
+    case OPENMINI_QMM_Q4_K: return dispatch_kind<OPENMINI_QMM_Q4_K>(grp, w0, x, batch, count, swiglu, s);
+    case OPENMINI_QMM_Q6_K: return dispatch_kind<OPENMINI_QMM_Q6_K>(grp, w0, x, batch, count, swiglu, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv(const Weight& w, const float* x, float* y, int batch, hipStream_t s) {

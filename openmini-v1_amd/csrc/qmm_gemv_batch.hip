@@ -316,8 +316,9 @@ hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int
 
 }  // namespace
 
+// Q4_K / Q6_K weights run the single-row kernel at every batch (one launch per 4 rows).
 bool use_batch_kernel(const Weight& w, int64_t batch) {
-    return batch >= kBatchMin && (int64_t)kBatchRows * w.k * 4 <= INT32_MAX;
+    return batch >= kBatchMin && !is_kquant(w.type) && (int64_t)kBatchRows * w.k * 4 <= INT32_MAX;
 }
 
 hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, float* y, int64_t batch,

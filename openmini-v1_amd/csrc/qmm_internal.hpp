@@ -26,6 +26,23 @@
 // so (w << 4) & 0xF0F0F0F0 and w & 0xF0F0F0F0 are 16 * (q - 8) of elements
 // 8j..8j+3 and 8j+4..8j+7 as int8 bytes, in order (ready-made int8 MFMA operands),
 // and v_cvt_off_f32_i4 turns a nibble into (q - 8) / 16 in one op.
+//
+// K-quant weights (decode GEMV only) use the same tiles with 32-element sub-blocks as
+// the "blocks" (a 256-element super-block = 8 sub-blocks = 2 groups, so K % 256 == 0):
+//   Q4_K (144-byte super-blocks, reference reading quant.rs:338-410): element value
+//     (q - 8) * d * scale + dmin * 0 (the reference's minimum is always 0); both
+//     products are exact, so the value is (q - 8) * (d * scale).  Slot codes as Q4_0
+//     (16 B of nibbles q ^ 8); then 64 x u8 scale (scales[sb] & 0x3F); then 16 x fp16 d,
+//     one per row of the tile (d becomes NaN when dmin is not finite, as every value
+//     of that super-block is then NaN).  1120 B per chunk.
+//   Q6_K (210-byte super-blocks, quant.rs:515-600): element value q * d * scale16 with
+//     q = low + 16 * high - 32 in [-32, 31] and a signed 8-bit scale per 16 elements,
+//     again exact as q * (d * scale16).  Slot codes: 16 B of the low 4 bits of the
+//     6-bit two's-complement code v = q & 63, packed as Q4_0's nibbles (word j, byte i:
+//     low nibble element 8j + i, high nibble 8j + 4 + i), then 8 B of its top 2 bits
+//     (word m, byte i, bits 2f..2f+1: element 16m + 4f + i); then 64 x 2 int8 scales
+//     (the slot's two 16-element halves); then 16 x fp16 d.  1696 B per chunk.
+//     (w << 2) & 0x3C3C3C3C | (hi << s) & 0xC0C0C0C0 is then 4 q per int8 byte.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -48,9 +65,21 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
-inline int bytes_per_block(int type) {
-    return type == OPENMINI_QMM_Q4_0 ? 18 : type == OPENMINI_QMM_Q8_0 ? 34 : 0;
+// GGUF block geometry of the weight layouts (upload, GEMV; the GEMM takes Q4_0 and
+// Q8_0 only): elements and bytes per GGUF block.
+inline int weight_block_elems(int type) {
+    return (type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q6_K) ? 256 : 32;
 }
+inline int bytes_per_block(int type) {
+    switch (type) {
+    case OPENMINI_QMM_Q4_0: return 18;
+    case OPENMINI_QMM_Q8_0: return 34;
+    case OPENMINI_QMM_Q4_K: return 144;
+    case OPENMINI_QMM_Q6_K: return 210;
+    default: return 0;
+    }
+}
+inline bool is_kquant(int type) { return type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q6_K; }
 
 // GgufTensorType::{block_size, bytes_per_block} (src/model/inference/gguf.rs:348-379)
 // for the layouts the dequantization entry points accept; 0 for others.
@@ -85,7 +114,13 @@ constexpr int kTileEntries = kTileRows * kTileBlocks;  // slots per chunk
 
 // Bytes of one chunk: 64 slots of codes, then their 64 fp16 scales.
 __host__ __device__ constexpr int chunk_bytes_for(bool q4) { return kTileEntries * (q4 ? 16 : 32) + 2 * kTileEntries; }
-inline int chunk_bytes(int type) { return chunk_bytes_for(type == OPENMINI_QMM_Q4_0); }
+// K-quant chunks: codes, per-slot scale bytes, then one fp16 d per tile row.
+constexpr int kQ4KChunk = kTileEntries * 16 + kTileEntries + 2 * kTileRows;       // 1120
+constexpr int kQ6KChunk = kTileEntries * 24 + 2 * kTileEntries + 2 * kTileRows;   // 1696
+inline int chunk_bytes(int type) {
+    return type == OPENMINI_QMM_Q4_K ? kQ4KChunk : type == OPENMINI_QMM_Q6_K ? kQ6KChunk
+                                                                           : chunk_bytes_for(type == OPENMINI_QMM_Q4_0);
+}
 
 // Chunk index and slot of (row, blk).
 __host__ __device__ __forceinline__ int64_t chunk_of(int64_t row, int64_t blk, int64_t groups) {

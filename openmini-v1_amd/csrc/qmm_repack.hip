@@ -99,6 +99,96 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
     if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
+// K-quant super-blocks -> chunks (layouts in qmm_internal.hpp).  One thread per chunk
+// slot, consecutive threads consecutive slots of a chunk, so a wave writes a chunk's
+// codes as one contiguous span; every byte of the chunk array is written (padding
+// rows as zeros).  Super-block reading as the reference's (paths relative to
+// openmini-server/src/model/inference/):
+//   Q4_K quant.rs:338-410: d = fp16 at 0, dmin = fp16 at 2, scale of sub-block sb =
+//        byte 4 + sb & 0x3F, codes from byte 12 (sub-block sb: 16 bytes at 12 + 16 sb,
+//        element 2j in the high nibble of byte j as in Q4_0), minimum always 0.
+//   Q6_K quant.rs:515-600: d = fp16 at 0; element i: low = nibble of byte 2 + i / 2
+//        (even i: low nibble), high = bits 2 (i % 4) of byte 66 + i / 4,
+//        q = low + 16 high - 32, scale = int8 byte 130 + i / 16.
+template <int kType>
+__global__ __launch_bounds__(256) void repack_kquant_kernel(const uint8_t* __restrict__ gguf, int64_t n,
+                                                            int64_t supers, int64_t groups, int64_t slots,
+                                                            uint8_t* __restrict__ chunks) {
+    constexpr bool kQ6 = kType == OPENMINI_QMM_Q6_K;
+    constexpr int kBPB = kQ6 ? 210 : 144;
+    constexpr int kChunk = kQ6 ? kQ6KChunk : kQ4KChunk;
+    constexpr int kScaleOff = kQ6 ? kTileEntries * 24 : kTileEntries * 16;
+    constexpr int kDOff = kScaleOff + (kQ6 ? 2 : 1) * kTileEntries;
+    const int64_t gs = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gs >= slots) return;
+    const int64_t c = gs / kTileEntries;
+    const int e = (int)(gs % kTileEntries), r = e & 15, t = e >> 4;
+    const int64_t rt = c / groups, g = c % groups;
+    const int64_t row = rt * kTileRows + r;
+    const int sub = (int)(g & 1) * kTileBlocks + t;  // 32-element sub-block of super-block g / 2
+    uint8_t* ch = chunks + c * kChunk;
+    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t sc = 0;
+    uint16_t dbits = 0;
+    if (row < n) {
+        const uint8_t* blk = gguf + (row * supers + (g >> 1)) * kBPB;
+        const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+        if constexpr (!kQ6) {
+            const uint8_t* qs = blk + 12 + sub * 16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v |= (q4_code(qs, 8 * j + i) | (q4_code(qs, 8 * j + 4 + i) << 4)) << (8 * i);
+                w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
+            }
+            sc = blk[4 + sub] & 0x3Fu;
+            // dmin * 0 is NaN for an inf / NaN dmin, and so is every value of the block
+            const uint16_t dmin = (uint16_t)(blk[2] | (blk[3] << 8));
+            dbits = (dmin & 0x7C00u) == 0x7C00u ? (uint16_t)0x7E00u : d;
+        } else {
+            const uint8_t* ql = blk + 2;
+            const uint8_t* qh = blk + 66;
+            uint32_t lo4[32], hi2[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int el = sub * 32 + i;
+                lo4[i] = (el & 1) ? (ql[el >> 1] >> 4) : (ql[el >> 1] & 0x0Fu);
+                // v = q & 63 = low + 16 ((high + 2) & 3): the top bits are high ^ 2
+                hi2[i] = ((qh[el >> 2] >> ((el & 3) * 2)) & 3u) ^ 2u;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v |= (lo4[8 * j + i] | (lo4[8 * j + 4 + i] << 4)) << (8 * i);
+                w[j] = v;
+            }
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int f = 0; f < 4; ++f) v |= hi2[16 * m + 4 * f + i] << (8 * i + 2 * f);
+                w[4 + m] = v;
+            }
+            sc = (uint32_t)blk[130 + 2 * sub] | ((uint32_t)blk[131 + 2 * sub] << 8);
+            dbits = d;
+        }
+    }
+    if constexpr (!kQ6) {
+        reinterpret_cast<uint4*>(ch)[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        ch[kScaleOff + e] = (uint8_t)sc;
+    } else {
+        reinterpret_cast<uint4*>(ch)[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        reinterpret_cast<uint2*>(ch + kTileEntries * 16)[e] = make_uint2(w[4], w[5]);
+        reinterpret_cast<uint16_t*>(ch + kScaleOff)[e] = (uint16_t)sc;
+    }
+    if (t == 0) reinterpret_cast<uint16_t*>(ch + kDOff)[r] = dbits;
+}
+
 // Chunked weight -> f32 [n][k] (8 * nwords outputs, row-major; one code word = 8
 // consecutive elements of a row).  A wave covers 512 consecutive outputs: lane l
 // decodes the half-word of four at 4 l and the one at 256 + 4 l, so each of its two
@@ -421,6 +511,17 @@ inline unsigned grid_for(int64_t items, int per_block) {
 
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
     if (w.n_tiles <= 0 || w.groups <= 0) return hipSuccess;
+    if (is_kquant(w.type)) {
+        const int64_t slots = w.n_tiles * w.groups * kTileEntries;
+        const dim3 grid((unsigned)((slots + 255) / 256));
+        if (w.type == OPENMINI_QMM_Q4_K)
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q4_K>, grid, dim3(256), 0, s, gguf, w.n, w.k / 256,
+                               w.groups, slots, w.chunks);
+        else
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q6_K>, grid, dim3(256), 0, s, gguf, w.n, w.k / 256,
+                               w.groups, slots, w.chunks);
+        return hipGetLastError();
+    }
     const int aligned = ((uintptr_t)gguf % 16) == 0 && w.nb % 8 == 0;
     const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
     const dim3 grid((unsigned)(w.n_tiles * quads));

@@ -79,3 +79,29 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
 def weight_blocks(qtype: int, n_rows: int, k_cols: int, seed: int, sigma: float = 0.02) -> np.ndarray:
     """GGUF blocks of W[n_rows, k_cols] ~ N(0, sigma), row-major (row n = K/32 blocks)."""
     return quantize(qtype, normal(seed, (n_rows, k_cols), sigma))
+
+
+Q4_K, Q6_K = 12, 14
+
+
+def kquant_blocks(qtype: int, n_rows: int, k_cols: int, seed: int) -> np.ndarray:
+    """Random GGUF Q4_K (144 B) / Q6_K (210 B) super-blocks of W[n_rows, k_cols], row n =
+    k_cols / 256 super-blocks, with finite fp16 d (and Q4_K dmin) of weight-like size
+    (values up to ~0.05).  The reference has no K-quant quantizer; these blocks exercise
+    its reading of the layouts (quant.rs:338-410, 515-600): every code and scale byte is
+    random, d and dmin are drawn small and positive or negative."""
+    assert k_cols % 256 == 0
+    rng = np.random.default_rng(seed)
+    nblk = n_rows * (k_cols // 256)
+    bpb = 144 if qtype == Q4_K else 210
+    raw = rng.integers(0, 256, size=(nblk, bpb), dtype=np.uint8)
+    sign = np.where(rng.random(nblk) < 0.5, -1.0, 1.0)
+    if qtype == Q4_K:
+        d = (sign * (rng.random(nblk) * 1e-4 + 2e-5)).astype(np.float16)
+        dmin = (rng.standard_normal(nblk) * 1e-3).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        raw[:, 2:4] = dmin.view(np.uint8).reshape(-1, 2)
+    else:
+        d = (sign * (rng.random(nblk) * 2e-5 + 5e-6)).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    return raw.ravel()

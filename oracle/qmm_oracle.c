@@ -525,11 +525,11 @@ void orc_quantize_q8_0(const float *x, size_t n, uint8_t *out) {
 
 /* ---- the contraction (src/model/inference/model.rs:1050-1064) -------------
  * linear(x, W) = x . W^T with W[N,K] stored as GGUF blocks, row n = K/32
- * consecutive blocks.  Dequantized with quant::dequantize, accumulated in fp64:
+ * consecutive blocks (K/256 super-blocks for the K-quants).  Dequantized with quant::dequantize, accumulated in fp64:
  *   y[b, n] = sum_k x[b, k] * w[n, k]. */
 static void dequant_row(int type, const uint8_t *w, size_t K, size_t n, float *row) {
     size_t bpb = orc_bytes_per_block(type);
-    size_t row_bytes = (K / QK) * bpb;
+    size_t row_bytes = (K / orc_block_size(type)) * bpb; /* 32 or 256 (K-quant super-blocks) */
     orc_dequantize(type, w + n * row_bytes, row_bytes, K, row);
 }
 

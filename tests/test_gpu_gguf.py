@@ -62,7 +62,7 @@ def test_tensor_by_ref_every_layout(qmm, orc, tmp_path):
         got = g.get_tensor_data_by_ref(g.tensors[name])
         ref = orc.dequantize(t, np.frombuffer(raw, np.uint8), dims[0])
         assert np.array_equal(bits(got), bits(ref)), name
-    with pytest.raises(G.GgufError):  # K-quant weights are dequantized, not uploaded
+    with pytest.raises(G.GgufError):  # a 1-D tensor is not a linear weight
         g.upload_weight("t12")
 
 

@@ -1,0 +1,143 @@
+"""Decode GEMV on Q4_K / Q6_K weights, read the way the reference reads those blocks
+(openmini-server/src/model/inference/quant.rs:338-410 and :515-600; the Q4_K minimum
+is always 0 there), against the fp64 oracle over orc_dequantize_q4_k / _q6_k
+(model.rs:1050-1064 semantics, y = x . W^T; tolerance from tests/parity.py).
+
+The weights stay in their K-quant form on the GPU (repacked codes, per-sub-block
+scales, one d per row and super-block); the element values are exact products of an
+integer code and an fp32 factor, which the one-hot test checks bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gguf_fixtures as fx
+from openmini_qmm import _native, synth
+from openmini_qmm import gguf as G
+from parity import TOL, assert_parity
+
+pytestmark = pytest.mark.gpu
+Q4_K, Q6_K = 12, 14
+BPB = {Q4_K: 144, Q6_K: 210}
+
+
+def gemv_nan_filled(qmm, w, x):
+    B = x.shape[0]
+    dx = qmm.DeviceBuffer.from_numpy(np.ascontiguousarray(x))
+    dy = qmm.DeviceBuffer(B * w.n_rows * 4)
+    dy.fill(0xFF)  # NaN: a row the kernel does not write fails the check
+    w.gemv(dx, dy, B)
+    return dy.download(np.float32, (B, w.n_rows))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K", [(1, 256), (37, 512), (130, 2304), (300, 4096)])
+@pytest.mark.parametrize("B", [1, 2, 4, 5])
+def test_kquant_gemv_parity(qmm, orc, qtype, N, K, B):
+    print(f"kquant gemv type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC000 + N + K + B)
+    x = synth.normal(0xC001 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    assert_parity(gemv_nan_filled(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} K={K} B={B}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K", [(4096, 11008), (11008, 4096)])
+@pytest.mark.parametrize("B", [1, 4])
+def test_kquant_gemv_llama_shapes(qmm, orc, qtype, N, K, B):
+    """The Llama-7B down (4096 x 11008) and up (11008 x 4096) projections."""
+    print(f"kquant gemv type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC100 + N + B)
+    x = synth.normal(0xC101 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    print(assert_parity(gemv_nan_filled(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, "llama"))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_one_hot_columns_exact(qmm, orc, qtype):
+    """x = e_k makes y = W[:, k] exactly: the activation's block is 2^29 e_k in one digit,
+    the code's integer dot product is exact, and code * (d * scale) equals the
+    reference's (code * d) * scale (both exact).  Columns at sub-block, half and
+    super-block edges of the first, a middle and the last super-block."""
+    N, K = 77, 1024
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC200 + qtype)
+    W = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    cols = [0, 15, 16, 31, 32, 255, 256, 511, 700, 1023]
+    x = np.zeros((len(cols), K), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    y = np.concatenate([gemv_nan_filled(qmm, w, x[i:i + 4]) for i in range(0, len(cols), 4)])
+    for i, c in enumerate(cols):
+        assert np.array_equal(y[i], W[:, c]), (c, np.nonzero(y[i] != W[:, c]))
+
+
+def test_q4_k_nonfinite_dmin_poisons_its_rows(qmm, orc):
+    """An inf / NaN dmin makes every value of its super-block NaN in the reference
+    (dmin * 0.0, quant.rs:376-385), so exactly the outputs of that row are NaN."""
+    N, K = 48, 768
+    blocks = synth.kquant_blocks(Q4_K, N, K, seed=0xC300).reshape(N, K // 256, 144)
+    blocks[5, 1, 2:4] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)
+    blocks[20, 2, 2:4] = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)
+    blocks = blocks.ravel()
+    w = qmm.QuantizedWeight(Q4_K, blocks, N, K)
+    x = synth.normal(0xC301, (2, K), 1.0)
+    y = gemv_nan_filled(qmm, w, x)
+    with np.errstate(invalid="ignore"):
+        ref = orc.linear_f64(Q4_K, blocks, N, K, x)
+    bad = [5, 20]
+    assert not np.any(np.isfinite(ref[:, bad])) and not np.any(np.isfinite(y[:, bad]))
+    good = [n for n in range(N) if n not in bad]
+    assert_parity(y[:, good], ref[:, good], TOL, "finite rows")
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_layer_calls(qmm, orc, qtype):
+    """gemv_multi (q / k / v sharing x) and the FFN hidden state silu(gate) * up on
+    K-quant weights, at batch 1 and at batch 6 (routed to launches of up to 4 rows)."""
+    H, F = 512, 1280
+    bq, bk = synth.kquant_blocks(qtype, H, H, 0xC400), synth.kquant_blocks(qtype, 256, H, 0xC401)
+    bg, bu = synth.kquant_blocks(qtype, F, H, 0xC402), synth.kquant_blocks(qtype, F, H, 0xC403)
+    wq, wk = qmm.QuantizedWeight(qtype, bq, H, H), qmm.QuantizedWeight(qtype, bk, 256, H)
+    wg, wu = qmm.QuantizedWeight(qtype, bg, F, H), qmm.QuantizedWeight(qtype, bu, F, H)
+    for B in (1, 6):
+        x = synth.normal(0xC410 + B, (B, H), 1.0)
+        dx = qmm.DeviceBuffer.from_numpy(x)
+        dq, dk = qmm.DeviceBuffer(B * H * 4), qmm.DeviceBuffer(B * 256 * 4)
+        qmm.gemv_multi((wq, wk), dx, (dq, dk), B)
+        assert_parity(dq.download(np.float32, (B, H)), orc.linear_f64(qtype, bq, H, H, x), TOL, "q")
+        assert_parity(dk.download(np.float32, (B, 256)), orc.linear_f64(qtype, bk, 256, H, x), TOL, "k")
+        dh = qmm.DeviceBuffer(B * F * 4)
+        qmm.ffn_gate_up(wg, wu, dx, dh, B)
+        assert_parity(dh.download(np.float32, (B, F)), orc.ffn_hidden_f64(qtype, bg, bu, F, H, x), TOL, "hidden")
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_from_gguf_file(qmm, tmp_path, qtype):
+    """A K-quant projection read from a GGUF file uploads as its raw super-blocks and
+    gives exactly what the same bytes give through openmini_qmm_upload."""
+    N, K = 96, 1536
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC500 + qtype)
+    path = tmp_path / "kq.gguf"
+    path.write_bytes(fx.build([("general.architecture", fx.STRING, "llama")],
+                              [("model.layers.0.ffn.up_proj", [K, N], qtype, blocks.tobytes())], "standard"))
+    w_file = G.GgufFile(str(path)).upload_weight("model.layers.0.ffn.up_proj")
+    w_direct = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(0xC501, (3, K), 1.0)
+    assert np.array_equal(gemv_nan_filled(qmm, w_file, x), gemv_nan_filled(qmm, w_direct, x))
+
+
+def test_kquant_error_paths(qmm):
+    L = _native.lib()
+    blocks = synth.kquant_blocks(Q4_K, 16, 512, seed=0xC600)
+    h = ctypes.c_void_p()
+    ptr = blocks.ctypes.data_as(ctypes.c_void_p)
+    # K must be a multiple of the 256-element super-block
+    assert L.openmini_qmm_upload(Q4_K, ptr, blocks.size, 32, 256 + 32, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
+    # 16 rows of K = 512 need 16 * 2 * 144 bytes
+    assert L.openmini_qmm_upload(Q4_K, ptr, blocks.size - 1, 16, 512, ctypes.byref(h)) \
+        == _native.ERR_INSUFFICIENT_DATA
+    w = qmm.QuantizedWeight(Q4_K, blocks, 16, 512)
+    assert w.info().gguf_bytes == 16 * 2 * 144
+    dx, dy = qmm.DeviceBuffer(16 * 512 * 2), qmm.DeviceBuffer(16 * 16 * 4)
+    assert L.openmini_qmm_gemm_bf16(w.handle, dx.ptr, dy.ptr, 16, None) == _native.ERR_UNSUPPORTED
+    assert L.openmini_qmm_dequant_weight(w.handle, dy.ptr, None) == _native.ERR_UNSUPPORTED

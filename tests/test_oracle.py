@@ -295,6 +295,22 @@ def test_linear_f64_matches_numpy_float64(orc, qtype):
     assert np.allclose(got_b, ref_b, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("qtype", [12, 14])
+def test_linear_f64_kquant_rows(orc, qtype):
+    """K-quant weights: row n of W[N, K] is its own K / 256 super-blocks (GGUF ne0 = K
+    contiguous).  Each output must equal the fp64 dot of x with that row dequantized on
+    its own, so a row stride of K / 32 blocks (the Q4_0 geometry) fails."""
+    N, K, B = 6, 768, 2
+    bpb = 144 if qtype == 12 else 210
+    blocks = synth.kquant_blocks(qtype, N, K, seed=21 + qtype)
+    x = synth.normal(22, (B, K), 1.0)
+    got = orc.linear_f64(qtype, blocks, N, K, x)
+    row_bytes = K // 256 * bpb
+    for n in range(N):
+        wr = orc.dequantize(qtype, blocks[n * row_bytes:(n + 1) * row_bytes], K).astype(np.float64)
+        assert np.allclose(got[:, n], x.astype(np.float64) @ wr, rtol=1e-12, atol=1e-12), n
+
+
 def test_linear_closed_form(orc):
     # every code 0x99 -> q = 9 - 8 = 1, d = 0.5: w = 0.5 everywhere; x = 1 -> y = 0.5 K
     K, N = 96, 3
