@@ -235,7 +235,10 @@ int openmini_qmm_dequantize(int type, const void* gguf, size_t gguf_bytes, size_
  * dequantize_simd :304-313), for F32, F16, Q4_0, Q4_1, Q8_0 and Q2_K..Q8_K: the blocks
  * that fit in gguf_bytes are dequantized, the rest of the n outputs are 0.0 (the
  * reference stops at the first incomplete block).  Bit-identical to the reference,
- * signed zeros included.  Other type ids -> UNSUPPORTED (the reference returns zeros
+ * signed zeros included.  F32 / F16 input with fewer than n whole elements: those
+ * elements, then 0.0 -- dequantize_simd's fixed-length result (quant_simd.rs:332-340);
+ * quant::dequantize_f32 / _f16 (quant.rs:95-133) return the same leading values as a
+ * shorter vector.  Other type ids -> UNSUPPORTED (the reference returns zeros
  * for types it does not implement; the IQ types are not implemented here). */
 int openmini_qmm_dequantize_any_device(int type, const void* d_gguf, size_t gguf_bytes, size_t n,
                                        float* d_out, void* stream);
@@ -337,7 +340,11 @@ int openmini_qmm_gguf_upload_weight(const openmini_qmm_gguf_t* gguf, const char*
 
 /* GgufFile::get_tensor_data_by_ref (gguf.rs:2062-2110) on the GPU: the tensor as
  * n_elements f32 in device memory at d_out, bit-identical to the reference for F32, F16,
- * Q4_0, Q4_1, Q8_0 and Q2_K..Q8_K (UNSUPPORTED for other types).  Synchronous. */
+ * Q4_0, Q4_1, Q8_0 and Q2_K..Q8_K (UNSUPPORTED for other types).  Synchronous.
+ * As the reference, an F32 tensor whose data does not start 4-byte aligned in the file,
+ * or an F16 tensor not 2-byte aligned, is MODEL_LOAD "F32 data is not properly aligned" /
+ * "F16 data is not properly aligned" (gguf.rs:2076-2078, 2090-2092; the reference's
+ * size-mismatch errors cannot occur: data_size is n_elements * 4 | 2 by definition). */
 int openmini_qmm_gguf_dequantize_tensor(const openmini_qmm_gguf_t* gguf, const char* name, float* d_out,
                                         void* stream);
 

@@ -1,9 +1,14 @@
 """Builds libopenmini_qmm.so for gfx950 with hipcc (in-tree, next to this file).
 
     python openmini-v1_amd/build.py            # compile every source, then link
+    python openmini-v1_amd/build.py --asan     # host code with AddressSanitizer:
+                                               # _build/asan/libopenmini_qmm_asan.so
 
 Each .hip source compiles to its own object in parallel; the shared library
-exports only the C-ABI declared in include/openmini_qmm.h.
+exports only the C-ABI declared in include/openmini_qmm.h.  The ASan variant
+instruments host code only (every -fsanitize= goes after -Xarch_host; device code is
+the same as the release build) and needs the clang ASan runtime preloaded
+(asan_runtime() names it); tests/test_gguf_asan.py runs the GGUF parser fuzz on it.
 """
 from __future__ import annotations
 
@@ -38,31 +43,47 @@ COMMON = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+ASAN_DIR = os.path.join(BUILD_DIR, "asan")
+ASAN_LIB_PATH = os.path.join(ASAN_DIR, "libopenmini_qmm_asan.so")
+# host pass only: each sanitizer option preceded by -Xarch_host
+ASAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def asan_runtime() -> str:
+    """The clang ASan runtime a process must preload to load the ASan variant."""
+    found = sorted(glob.glob("/opt/rocm/lib/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError("clang ASan runtime not found under /opt/rocm/lib/llvm")
+    return found[-1]
+
+
+def _compile(src: str, out_dir: str = BUILD_DIR, extra=()) -> str:
+    obj = os.path.join(out_dir, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *COMMON, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD_DIR, exist_ok=True)
+def build(verbose: bool = False, asan: bool = False) -> str:
+    out_dir, lib_path = (ASAN_DIR, ASAN_LIB_PATH) if asan else (BUILD_DIR, LIB_PATH)
+    extra = ASAN_HOST if asan else ()
+    os.makedirs(out_dir, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+        objs = list(ex.map(lambda src: _compile(src, out_dir, extra), sources))
+    tmp = lib_path + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *extra, "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH}")
-    return LIB_PATH
+        print(f"built {lib_path}")
+    return lib_path
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, asan="--asan" in sys.argv[1:])
     sys.exit(0)

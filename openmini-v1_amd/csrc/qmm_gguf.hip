@@ -240,7 +240,9 @@ bool parse_value_of(Cursor& c, uint32_t type, bool one_byte, bool allow_array, V
             c.err = "Unexpected EOF while reading array";
             return false;
         }
-        v->arr.reserve((size_t)count);
+        // the count is bounded only by the bytes left, which a corrupt file can make huge:
+        // reserve at most 64 Ki elements up front and let the vector grow past that
+        v->arr.reserve((size_t)(count < ((uint64_t)1 << 16) ? count : ((uint64_t)1 << 16)));
         for (uint64_t k = 0; k < count; ++k) {
             Value e;
             if (!parse_value_of(c, et, one_byte, false, &e)) return false;
@@ -423,25 +425,30 @@ int openmini_qmm_gguf_open(const char* path, int dialect, openmini_qmm_gguf_t** 
     g->size = size;
     std::string err;
     bool ok = false;
-    if (dialect == OPENMINI_QMM_GGUF_REFERENCE) {
-        ok = parse(*g, true, &err);
-        g->dialect = OPENMINI_QMM_GGUF_REFERENCE;
-    } else {
-        ok = parse(*g, false, &err);
-        g->dialect = OPENMINI_QMM_GGUF_STANDARD;
-        if (dialect == OPENMINI_QMM_GGUF_AUTO) {
-            bool all_fit = ok;
-            for (const auto& t : g->tensors) all_fit = all_fit && fits(*g, t);
-            if (!all_fit) {
-                std::string err2;
-                if (parse(*g, true, &err2)) {
-                    ok = true;
-                    g->dialect = OPENMINI_QMM_GGUF_REFERENCE;
-                } else if (ok) {
-                    parse(*g, false, &err);  // keep the standard reading
+    try {  // a file whose counts outrun host memory fails with MEMORY; nothing escapes the C ABI
+        if (dialect == OPENMINI_QMM_GGUF_REFERENCE) {
+            ok = parse(*g, true, &err);
+            g->dialect = OPENMINI_QMM_GGUF_REFERENCE;
+        } else {
+            ok = parse(*g, false, &err);
+            g->dialect = OPENMINI_QMM_GGUF_STANDARD;
+            if (dialect == OPENMINI_QMM_GGUF_AUTO) {
+                bool all_fit = ok;
+                for (const auto& t : g->tensors) all_fit = all_fit && fits(*g, t);
+                if (!all_fit) {
+                    std::string err2;
+                    if (parse(*g, true, &err2)) {
+                        ok = true;
+                        g->dialect = OPENMINI_QMM_GGUF_REFERENCE;
+                    } else if (ok) {
+                        parse(*g, false, &err);  // keep the standard reading
+                    }
                 }
             }
         }
+    } catch (const std::bad_alloc&) {
+        openmini_qmm_gguf_close(g);
+        return gfail(OPENMINI_QMM_ERR_MEMORY, "host allocation failed while parsing %s", path);
     }
     if (!ok) {
         openmini_qmm_gguf_close(g);
@@ -592,6 +599,12 @@ int openmini_qmm_gguf_dequantize_tensor(const openmini_qmm_gguf_t* g, const char
     if (!fits(*g, *t)) return gfail(OPENMINI_QMM_ERR_MODEL_LOAD, "Tensor data out of bounds");
     if (!qmm::layout_block_size(t->type))
         return gfail(OPENMINI_QMM_ERR_UNSUPPORTED, "%s is tensor type %d, which is not implemented", name, t->type);
+    // the reference casts F32 / F16 data in place and refuses a misaligned start (the
+    // mapping itself is page-aligned, so the file offset decides; gguf.rs:2074-2095)
+    if (t->type == OPENMINI_QMM_F32 && t->offset % 4 != 0)
+        return gfail(OPENMINI_QMM_ERR_MODEL_LOAD, "F32 data is not properly aligned");
+    if (t->type == OPENMINI_QMM_F16 && t->offset % 2 != 0)
+        return gfail(OPENMINI_QMM_ERR_MODEL_LOAD, "F16 data is not properly aligned");
     return qmm::dequantize_from_host(t->type, g->base + t->offset, (size_t)data_size_of(*t),
                                      (size_t)elements_of(*t), d_out, stream);
 }

@@ -336,11 +336,17 @@ __device__ __forceinline__ float elem(const uint8_t* b, int i) {
 }
 
 // Four outputs at element e (a multiple of 4) of one block.  Q4_0 / Q8_0
-// (quant.rs:152-195, 282-316) read the scale and codes as halfwords: blocks of 18 / 34
-// bytes start on even addresses.  Past n or past the blocks given: zeros.
+// (quant.rs:152-195, 282-316) read the scale and codes as halfwords when the source
+// starts on an even address (blocks of 18 / 34 bytes then all do), else byte by byte
+// (a tensor of the reference's GGUF dialect can sit at an odd file offset).  Past n or
+// past the blocks given: zeros.
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p, bool even) {
+    return even ? *reinterpret_cast<const uint16_t*>(p) : (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
 template <int kType>
 __device__ __forceinline__ void four_values(const uint8_t* __restrict__ gguf, size_t e, size_t n,
-                                            size_t avail_blocks, float* v) {
+                                            size_t avail_blocks, bool even, float* v) {
     using L = Layout<kType>;
     const size_t blk = e / L::kQ;
     const int i0 = (int)(e % L::kQ);
@@ -350,9 +356,8 @@ __device__ __forceinline__ void four_values(const uint8_t* __restrict__ gguf, si
     }
     const uint8_t* b = gguf + blk * L::kB;
     if constexpr (kType == OPENMINI_QMM_Q4_0) {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
-        const float d = f16_bits_to_f32(h[0]);
-        const uint32_t w = h[1 + i0 / 4];  // elements 2j (high nibble), 2j + 1 (low) of byte j
+        const float d = f16_bits_to_f32((uint16_t)ld_u16(b, even));
+        const uint32_t w = ld_u16(b + 2 + 2 * (i0 / 4), even);  // elements 2j (high nibble), 2j + 1 (low) of byte j
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const uint32_t c = (w >> (8 * t)) & 0xFFu;
@@ -360,11 +365,10 @@ __device__ __forceinline__ void four_values(const uint8_t* __restrict__ gguf, si
             v[2 * t + 1] = (float)((int)(c & 0x0Fu) - 8) * d;
         }
     } else if constexpr (kType == OPENMINI_QMM_Q8_0) {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
-        const float d = f16_bits_to_f32(h[0]);
+        const float d = f16_bits_to_f32((uint16_t)ld_u16(b, even));
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            const uint32_t w = h[1 + i0 / 2 + p];
+            const uint32_t w = ld_u16(b + 2 + 2 * (i0 / 2 + p), even);
             v[2 * p] = (float)(int8_t)(w & 0xFFu) * d;
             v[2 * p + 1] = (float)(int8_t)(w >> 8) * d;
         }
@@ -386,11 +390,12 @@ __global__ __launch_bounds__(256) void dequant_layout_kernel(const uint8_t* __re
     if (ea >= n) return;
     typedef float f32x4v __attribute__((ext_vector_type(4)));
     const bool aligned = ((uintptr_t)out & 15) == 0;
+    const bool even = ((uintptr_t)gguf & 1) == 0;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         const size_t e = ea + 256 * half;
         float v[4];
-        four_values<kType>(gguf, e, n, avail_blocks, v);
+        four_values<kType>(gguf, e, n, avail_blocks, even, v);
         if (aligned && e + 4 <= n) {
             __builtin_nontemporal_store(f32x4v{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4v*>(out + e));
         } else {

@@ -225,7 +225,10 @@ class QuantizedWeight:
 def dequantize(data, tensor_type, n: int) -> np.ndarray:
     """quant::dequantize (quant.rs:56-79), which dequantize_simd (quant_simd.rs:304-313)
     matches value for value: the blocks that fit in `data` are dequantized, the rest
-    of the n outputs are 0.0; bit-identical to the reference.  Types the library does
+    of the n outputs are 0.0; bit-identical to the reference.  F32 / F16 input shorter
+    than n elements: the whole elements, then 0.0 (dequantize_simd's fixed-length
+    result, quant_simd.rs:332-340; quant::dequantize_f32 / _f16, quant.rs:95-133,
+    return the same leading values without the zero tail).  Types the library does
     not implement raise UnsupportedType (the reference returns zeros)."""
     tt = int(tensor_type)
     buf = _as_u8(data)
@@ -344,10 +347,11 @@ class HipQuantOps:
 # ---- GemmEngine sibling ------------------------------------------------------------------
 
 class HipQuantGemmEngine:
-    """Quantized sibling of trait GemmEngine (gemm_engine.rs:37-56): same shape of API
-    (name, backend_type, matmul, is_available), host arrays at the edge, the weight a
-    device handle created at load.  matmul(x, W) computes x . W^T for W[N, K], i.e.
-    what linear() feeds GemmEngine::matmul after its W.t() copy (model.rs:1050-1064)."""
+    """Quantized sibling of trait GemmEngine (gemm_engine.rs:37-56): the same surface
+    (name, backend_type, matmul, batched_matmul, fused_gemm_relu, fused_gemm_silu,
+    is_available), host arrays at the edge, the weight a device handle created at load.
+    matmul(x, W) computes x . W^T for W[N, K], i.e. what linear() feeds
+    GemmEngine::matmul after its W.t() copy (model.rs:1050-1064)."""
 
     def name(self) -> str:
         return "hip_quant"
@@ -365,6 +369,42 @@ class HipQuantGemmEngine:
         y = np.empty((x.shape[0], weight.n_rows), dtype=np.float32)
         check(lib().openmini_qmm_linear_host(weight.handle, _ptr(x), _ptr(y), x.shape[0]))
         return y
+
+    def batched_matmul(self, x: np.ndarray, weights) -> np.ndarray:
+        """GemmEngine::batched_matmul (gemm_engine.rs:73-96): slice i of x[B, M, K] times
+        W_i^T; "Batch dimension mismatch" when B differs from the number of weights."""
+        x = np.asarray(x, dtype=np.float32)
+        if x.ndim != 3 or x.shape[0] != len(weights):
+            raise InvalidInput(f"Batch dimension mismatch: {x.shape[0] if x.ndim == 3 else x.shape} "
+                               f"vs {len(weights)}")
+        n = {w.n_rows for w in weights}
+        if len(n) > 1:
+            raise InvalidInput("batched weights differ in N")
+        return np.stack([self.matmul(x[i], w) for i, w in enumerate(weights)]) if len(weights) else \
+            np.zeros((0, x.shape[1], 0), np.float32)
+
+    def fused_gemm_relu(self, x: np.ndarray, weight: QuantizedWeight, bias=None) -> np.ndarray:
+        """GemmEngine::fused_gemm_relu (gemm_engine.rs:98-110): relu(x . W^T + bias)."""
+        y = self.matmul(x, weight)
+        if bias is not None:
+            y = y + np.asarray(bias, dtype=np.float32)
+        return np.maximum(y, np.float32(0.0))
+
+    def fused_gemm_silu(self, x: np.ndarray, gate: QuantizedWeight, up: QuantizedWeight,
+                        bias=None) -> np.ndarray:
+        """FFNWeights::forward's hidden state silu(x . Wg^T) * (x . Wu^T) (+ bias)
+        (model.rs:728-731), gate and up in one launch (openmini_qmm_ffn_gate_up).  The
+        ndarray fallback's fused_gemm_silu (gemm_engine.rs:112-130) computes
+        gate * silu(up) on untransposed weights instead; that branch is not followed."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != gate.k_cols or (gate.n_rows, gate.k_cols) != (up.n_rows, up.k_cols):
+            raise InvalidInput(f"x {x.shape}, gate [{gate.n_rows}, {gate.k_cols}], up [{up.n_rows}, "
+                               f"{up.k_cols}] do not match")
+        dx = DeviceBuffer.from_numpy(x)
+        dh = DeviceBuffer(x.shape[0] * gate.n_rows * 4)
+        check(lib().openmini_qmm_ffn_gate_up(gate.handle, up.handle, dx.ptr, dh.ptr, x.shape[0], None))
+        h = dh.download(np.float32, (x.shape[0], gate.n_rows))
+        return h + np.asarray(bias, dtype=np.float32) if bias is not None else h
 
 
 _ENGINE = None

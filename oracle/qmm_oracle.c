@@ -380,9 +380,13 @@ void orc_dequantize_q8_k(const uint8_t *data, size_t len, size_t n, float *out) 
     }
 }
 
-/* quant::dequantize dispatcher, quant.rs:56-79 (F32 via dequantize_f32, F16 via
- * dequantize_f16; the IQ types are not restated here; other types -> zeros :78).
- * Returns 1 for a type restated here, 0 otherwise (output zeroed). */
+/* quant::dequantize dispatcher, quant.rs:56-79 (the IQ types are not restated here;
+ * other types -> zeros :78).  Returns 1 for a type restated here, 0 otherwise (output
+ * zeroed).  F32 / F16 with fewer than n whole elements in `len`: the whole ones, then
+ * 0.0 up to n -- the fixed-length result of dequantize_simd's F32 / F16 arms
+ * (quant_simd.rs:304-313, dequantize_f32_impl :332-340 `vec![0.0f32; n]`).
+ * quant::dequantize_f32 / _f16 (quant.rs:95-133) return the same leading values but
+ * a shorter Vec (no tail). */
 int orc_dequantize(int type, const uint8_t *data, size_t len, size_t n, float *out) {
     switch (type) {
     case ORC_Q4_0: orc_dequantize_q4_0(data, len, n, out); return 1;

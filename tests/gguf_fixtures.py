@@ -31,9 +31,10 @@ def _value(vtype: int, v, one_byte: bool) -> bytes:
     return struct.pack(_FMT[vtype], v)
 
 
-def build(metadata, tensors, dialect: str, version: int = 3, alignment: int = 32) -> bytes:
+def build(metadata, tensors, dialect: str, version: int = 3, alignment: int = 32, data_shift: int = 0) -> bytes:
     """metadata: [(key, vtype, value)]; tensors: [(name, dims (GGUF order), type id,
-    data bytes)]."""
+    data bytes)].  data_shift (reference dialect): each data block starts that many bytes
+    past its 32-byte boundary (the reference applies no alignment of its own)."""
     one = dialect == "reference"
     tid = (lambda t: struct.pack("<B", t)) if one else (lambda t: struct.pack("<I", t))
     buf = bytearray(struct.pack("<IIQQ", 0x46554747, version, len(tensors), len(metadata)))
@@ -45,7 +46,7 @@ def build(metadata, tensors, dialect: str, version: int = 3, alignment: int = 32
         pos = len(buf) + info_len
         offsets = []
         for _, _, _, data in tensors:
-            pos = (pos + 31) // 32 * 32
+            pos = (pos + 31) // 32 * 32 + data_shift
             offsets.append(pos)
             pos += len(data)
         for (name, dims, t, _), off in zip(tensors, offsets):
@@ -77,3 +78,30 @@ def build_minimal_gguf() -> bytes:
                   ("llama.block_count", U32, 32)],
                  [("model.token_embd.weight", [4096], 0, np.full(4096, 0.5, dtype=np.float32).tobytes())],
                  "reference")
+
+
+def mutations(seed: int, count: int):
+    """Fixed-seed mutants of a multi-tensor file in both dialects: (dialect name, bytes)
+    with byte overwrites, 64-bit counts / lengths / offsets set to extreme values, and
+    truncation."""
+    import random
+    rng = random.Random(seed)
+    q = np.random.default_rng(1).integers(0, 256, 2 * 18 * 4, dtype=np.uint8)
+    meta = [("general.architecture", STRING, "llama"), ("a", ARRAY, (U32, [1, 2])), ("f", F32, 1.5)]
+    tens = [("w", [64, 4], 2, q.tobytes()), ("x", [8], 0, bytes(32))]
+    bases = {"reference": build(meta, tens, "reference"), "standard": build(meta, tens, "standard")}
+    for _ in range(count):
+        dialect = rng.choice(sorted(bases))
+        b = bytearray(bases[dialect])
+        for _ in range(rng.randint(1, 6)):
+            pos = rng.randrange(len(b))
+            r = rng.random()
+            if r < 0.5:
+                b[pos] = rng.randrange(256)
+            elif r < 0.85 and pos + 8 <= len(b):
+                b[pos:pos + 8] = struct.pack("<Q", rng.choice([0, 1, 2**31, 2**32 - 1, 2**63, 2**64 - 1,
+                                                                rng.randrange(2**64)]))
+            else:
+                del b[pos:]
+                break
+        yield dialect, bytes(b)

@@ -236,33 +236,16 @@ def test_random_mutations_parse_or_fail_cleanly(tmp_path):
     """Fixed-seed mutation fuzzing of a multi-tensor file in both dialects: byte
     overwrites, 64-bit counts / lengths / offsets set to extreme values, truncation.
     Every file either parses (and its tensor views stay in the file) or raises
-    GgufError; nothing else escapes and nothing crashes."""
-    import random
-    rng = random.Random(20261202)
-    q = np.random.default_rng(1).integers(0, 256, 2 * 18 * 4, dtype=np.uint8)
-    meta = [("general.architecture", fx.STRING, "llama"), ("a", fx.ARRAY, (fx.U32, [1, 2])), ("f", fx.F32, 1.5)]
-    tens = [("w", [64, 4], 2, q.tobytes()), ("x", [8], 0, bytes(32))]
-    bases = {G.REFERENCE: fx.build(meta, tens, "reference"), G.STANDARD: fx.build(meta, tens, "standard")}
+    GgufError; nothing else escapes and nothing crashes.  The same mutants run under
+    host AddressSanitizer in tests/test_gguf_asan.py."""
+    dialects = {"reference": G.REFERENCE, "standard": G.STANDARD}
     path = write(tmp_path, b"")
     parsed = failed = 0
-    for _ in range(600):
-        dialect = rng.choice(sorted(bases))
-        b = bytearray(bases[dialect])
-        for _ in range(rng.randint(1, 6)):
-            pos = rng.randrange(len(b))
-            r = rng.random()
-            if r < 0.5:
-                b[pos] = rng.randrange(256)
-            elif r < 0.85 and pos + 8 <= len(b):
-                b[pos:pos + 8] = struct.pack("<Q", rng.choice([0, 1, 2**31, 2**32 - 1, 2**63, 2**64 - 1,
-                                                                rng.randrange(2**64)]))
-            else:
-                del b[pos:]
-                break
+    for dialect, b in fx.mutations(20261202, 600):
         with open(path, "wb") as f:
-            f.write(bytes(b))
+            f.write(b)
         try:
-            g = G.GgufFile(path, dialect)
+            g = G.GgufFile(path, dialects[dialect])
         except G.GgufError:
             failed += 1
             continue
@@ -283,3 +266,44 @@ def test_oversized_tensor_dims_are_out_of_bounds(tmp_path, dims):
     data = fx.build([], [("t", dims, 0, bytes(64))], "reference")
     g = G.GgufFile(write(tmp_path, data), G.REFERENCE)
     assert g.get_tensor_data("t") is None
+
+
+_HUGE_ARRAY_CHILD = r"""
+import ctypes, resource, sys
+sys.path[:0] = sys.argv[2:]
+from openmini_qmm import _native
+L = _native.lib()
+vm = 0
+for line in open("/proc/self/status"):
+    if line.startswith("VmSize:"):
+        vm = int(line.split()[1]) * 1024
+lim = vm + (2 << 30)
+resource.setrlimit(resource.RLIMIT_AS, (lim, lim))
+h = ctypes.c_void_p()
+rc = L.openmini_qmm_gguf_open(sys.argv[1].encode(), 2, ctypes.byref(h))
+print(rc, L.openmini_qmm_last_error().decode())
+"""
+
+
+def test_huge_array_count_fails_with_memory_error(tmp_path):
+    """A u8 metadata array whose count fits in the file but whose parsed values outrun
+    host memory (40 M elements, ~3.5 GB of parsed values against 2 GiB of address space
+    left) fails with MEMORY; std::bad_alloc does not escape openmini_qmm_gguf_open.  Run
+    in a child process with a capped address space."""
+    import subprocess
+    import sys
+    n = 40_000_000
+    path = tmp_path / "huge_array.gguf"
+    with open(path, "wb") as f:
+        f.write(struct.pack("<IIQQ", 0x46554747, 3, 0, 1))
+        f.write(struct.pack("<Q", 1) + b"a" + struct.pack("<IIQ", fx.ARRAY, fx.U8, n))
+        f.write(bytes(n))
+    import os
+    here = os.path.dirname(os.path.abspath(__file__))
+    paths = [os.path.dirname(here), os.path.join(os.path.dirname(here), "openmini-v1_amd")]
+    r = subprocess.run([sys.executable, "-c", _HUGE_ARRAY_CHILD, str(path), *paths],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    rc, msg = r.stdout.strip().split(" ", 1)
+    assert int(rc) == -1, r.stdout  # OPENMINI_QMM_ERR_MEMORY
+    assert "allocation" in msg

@@ -193,7 +193,7 @@ def test_reference_generators_non_aligned_and_truncated(qmm, orc):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
-@pytest.mark.parametrize("offset", [0, 2, 6])
+@pytest.mark.parametrize("offset", [0, 1, 2, 3, 6])
 def test_upload_from_device_any_alignment(qmm, orc, qtype, offset):
     """Repack from blocks already in HBM, including sources that are not 16-byte
     aligned (GGUF data offsets are only guaranteed 32-aligned in the file)."""
@@ -291,3 +291,42 @@ def test_convert_to_soa_layout_matches_oracle(qmm, orc, qtype):
                     (raw[: 17 * bpb + 3], 40 * 32), (raw, nblk * 64), (raw[:0], 64), (raw, 0)):
         got = qmm.convert_to_soa_layout(data, qtype, n)
         assert np.array_equal(got, orc.convert_to_soa(qtype, data, n)), (qtype, data.size, n)
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("offset", [1, 3])
+def test_device_dequantize_odd_source_address(qmm, orc, qtype, offset):
+    """Raw GGUF bytes at an odd device address (a tensor of the reference's dialect can
+    start at any file offset, and a device copy of the file keeps that offset): the
+    any-type and the safe device entry points read the scale and codes byte by byte."""
+    import ctypes
+    from openmini_qmm import _native
+    L = _native.lib()
+    n = 32 * 777 + 5
+    raw = random_blocks(qtype, (n + 31) // 32, seed=90 + offset)
+    staged = np.zeros(raw.size + 16, np.uint8)
+    staged[offset:offset + raw.size] = raw
+    dbuf = qmm.DeviceBuffer.from_numpy(staged)
+    src = ctypes.c_void_p(dbuf.ptr.value + offset)
+    ref = orc.dequantize(qtype, raw, n)
+    out = qmm.DeviceBuffer(n * 4)
+    _native.check(L.openmini_qmm_dequantize_any_device(qtype, src, raw.size, n, out.ptr, None))
+    assert np.array_equal(bits(out.download(np.float32, (n,))), bits(ref))
+    out2 = qmm.DeviceBuffer(n * 4)
+    _native.check(L.openmini_qmm_dequantize_device(qtype, src, raw.size, n, out2.ptr, None, None))
+    assert np.array_equal(bits(out2.download(np.float32, (n,))), bits(ref))
+
+
+def test_f32_f16_short_input_zero_tail(qmm, orc):
+    """F32 / F16 input holding fewer than n whole elements gives those elements, then
+    0.0: dequantize_simd's fixed-length result (quant_simd.rs:332-340).  The reference's
+    quant::dequantize_f32 / _f16 (quant.rs:95-133) return the same leading values
+    without the tail.  Stray bytes of an incomplete element are ignored."""
+    f32 = np.array([1.0, -2.5, 3.25], np.float32).tobytes() + bytes([0x00, 0x00, 0x80])
+    want32 = np.array([1.0, -2.5, 3.25, 0.0, 0.0, 0.0], np.float32)
+    assert np.array_equal(bits(qmm.dequantize(f32, 0, 6)), bits(want32))
+    assert np.array_equal(bits(orc.dequantize(0, np.frombuffer(f32, np.uint8), 6)), bits(want32))
+    f16 = np.array([1.0, -0.5], np.float16).tobytes() + bytes([0x3C])
+    want16 = np.array([1.0, -0.5, 0.0, 0.0], np.float32)
+    assert np.array_equal(bits(qmm.dequantize(f16, 1, 4)), bits(want16))
+    assert np.array_equal(bits(orc.dequantize(1, np.frombuffer(f16, np.uint8), 4)), bits(want16))

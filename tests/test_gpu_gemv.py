@@ -266,3 +266,30 @@ def test_gemv_error_within_fp32_path(qmm, orc, qtype, B):
         print(f"row {r}: gpu {e_gpu:.3e} f32 path {e_f32:.3e}")
         assert e_gpu <= 4.0 * e_f32, (r, e_gpu, e_f32)
         assert_parity(y[r:r + 1], ref[r:r + 1], TOL, f"row {r}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_engine_full_surface(qmm, orc, qtype):
+    """The rest of the GemmEngine surface (gemm_engine.rs:37-56): batched_matmul over one
+    weight per batch slice (and the reference's batch-mismatch error), fused_gemm_relu
+    with a bias, and fused_gemm_silu as FFNWeights::forward's silu(gate) * up."""
+    N, K, M = 160, 512, 6
+    bs = [synth.weight_blocks(qtype, N, K, seed=0xE00 + i) for i in range(3)]
+    ws = [qmm.QuantizedWeight(qtype, b, N, K) for b in bs]
+    eng = qmm.get_gemm_engine()
+    x3 = synth.normal(0xE10, (3, M, K), 1.0)
+    y3 = eng.batched_matmul(x3, ws)
+    for i in range(3):
+        assert_parity(y3[i], orc.linear_f64(qtype, bs[i], N, K, x3[i]), TOL, f"batched {i}")
+    with pytest.raises(qmm.InvalidInput, match="Batch dimension mismatch"):
+        eng.batched_matmul(x3, ws[:2])
+    x = x3[0]
+    bias = synth.normal(0xE11, (N,), 1.0)
+    ref = np.maximum(orc.linear_f64(qtype, bs[0], N, K, x) + bias, 0.0)
+    got = eng.fused_gemm_relu(x, ws[0], bias)
+    assert np.all(got >= 0.0)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-3 * float(np.max(np.abs(ref))))
+    h = eng.fused_gemm_silu(x, ws[1], ws[2])
+    assert_parity(h, orc.ffn_hidden_f64(qtype, bs[1], bs[2], N, K, x), TOL, "silu(gate) * up")
+    hb = eng.fused_gemm_silu(x, ws[1], ws[2], bias)
+    np.testing.assert_allclose(hb, h + bias, rtol=0, atol=0)

@@ -90,3 +90,24 @@ def test_loader_layer(qmm, orc, tmp_path):
         assert np.max(np.abs(y - ref)) <= 1e-3 * np.max(np.abs(ref))
     with pytest.raises(G.GgufError, match="Tensor not found"):
         loader.load_tensor("model.layers.1.ffn.up_proj")
+
+
+@pytest.mark.parametrize("ttype,shift,ok", [(0, 0, True), (0, 2, False), (0, 4, True),
+                                           (1, 0, True), (1, 1, False), (1, 2, True)])
+def test_tensor_by_ref_f32_f16_alignment(qmm, tmp_path, ttype, shift, ok):
+    """get_tensor_data_by_ref casts F32 / F16 data in place and refuses a start that is
+    not 4- / 2-byte aligned in the file ("F32 data is not properly aligned",
+    gguf.rs:2076-2078, 2090-2092); the reference dialect places data anywhere."""
+    vals = np.array([0.5, -1.25, 3.0, 1e-3], np.float32)
+    raw = vals.tobytes() if ttype == 0 else vals.astype(np.float16).tobytes()
+    path = tmp_path / "plain.gguf"
+    path.write_bytes(fx.build([], [("t", [4], ttype, raw)], "reference", data_shift=shift))
+    g = G.GgufFile(str(path), G.REFERENCE)
+    if ok:
+        got = g.get_tensor_data_by_ref(g.tensors["t"])
+        want = vals if ttype == 0 else vals.astype(np.float16).astype(np.float32)
+        assert np.array_equal(bits(got), bits(want))
+    else:
+        name = "F32" if ttype == 0 else "F16"
+        with pytest.raises(G.GgufError, match=f"{name} data is not properly aligned"):
+            g.get_tensor_data_by_ref(g.tensors["t"])

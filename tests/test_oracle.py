@@ -502,3 +502,16 @@ def test_ffn_hidden_composition(orc):
     h = orc.ffn_hidden_f64(Q4_0, wg, wu, N, K, x)
     np.testing.assert_allclose(h, g * expit(g) * u, rtol=1e-12)
     assert not np.allclose(h, u * expit(u) * g, rtol=1e-3)
+
+
+def test_f32_f16_short_input_kat(orc):
+    """KAT: F32 / F16 bytes holding fewer than n whole elements -> those elements, then
+    0.0 (dequantize_simd's fixed-length result, quant_simd.rs:332-340; quant.rs:95-133
+    returns the same leading values without the tail)."""
+    f32 = np.array([1.0, -2.5, 3.25], np.float32).tobytes() + bytes([0x00, 0x00, 0x80])
+    got = orc.dequantize(0, np.frombuffer(f32, np.uint8), 6)
+    assert np.array_equal(got.view(np.uint32),
+                          np.array([1.0, -2.5, 3.25, 0, 0, 0], np.float32).view(np.uint32))
+    f16 = np.array([1.0, -0.5], np.float16).tobytes() + bytes([0x3C])
+    got = orc.dequantize(1, np.frombuffer(f16, np.uint8), 4)
+    assert np.array_equal(got.view(np.uint32), np.array([1.0, -0.5, 0, 0], np.float32).view(np.uint32))
