@@ -366,8 +366,9 @@ int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void*
 
 /* Single-launch floor: a read-only streaming kernel over `bytes` (multiple of 16,
  * 16-byte aligned source) on `stream`, 16-byte loads, workgroups of 512 lanes over
- * consecutive 32 KB spans.  Nothing is written in practice; d_sink (4 bytes, 4-byte
- * aligned) receives a word only if the data fold hits a sentinel.  The time a
+ * consecutive 16 KB spans (the fastest read shape measured on MI355X).  Nothing is
+ * written in practice; d_sink (4 bytes, 4-byte aligned) receives a word only if the
+ * data fold hits a sentinel.  The time a
  * read-bound kernel of that many bytes cannot beat in one launch; the decode GEMV
  * is measured against it.  No counterpart in the reference. */
 int openmini_qmm_stream_read(const void* d_src, size_t bytes, void* d_sink, void* stream);

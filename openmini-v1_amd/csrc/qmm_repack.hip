@@ -466,10 +466,13 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* __restric
 }
 
 // Read-only streaming yardstick: every 16-byte word of src is read once (kReadU loads in
-// flight per lane, workgroups of 512 lanes over consecutive 32 KB spans), folded into a
+// flight per lane, workgroups of 512 lanes over consecutive 16 KB spans), folded into a
 // register, and nothing is stored unless a lane's fold equals a sentinel (which keeps
-// the loads live).  The single-launch floor a read-bound kernel of `bytes` meets.
-constexpr int kReadU = 4;
+// the loads live).  The single-launch floor a read-bound kernel of `bytes` meets.  The
+// shape is the fastest of a sweep on MI355X (1-16 loads per lane, 256-1024 lanes per
+// workgroup, strided or per-wave spans): at 25.4 MB, 2 loads x 512 lanes took 5.37 us
+// against 5.69 us for 4 x 512 and 5.79 us for 8 x 1024.
+constexpr int kReadU = 2;
 __global__ __launch_bounds__(512) void stream_read_kernel(const uint4* __restrict__ src, int64_t n16,
                                                           uint32_t* __restrict__ sink) {
     const int64_t base = (int64_t)blockIdx.x * (512 * kReadU) + threadIdx.x;
