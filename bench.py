@@ -525,6 +525,17 @@ def main(argv=None) -> int:
         log(f"stream copy {copy['bytes']} B: {copy['gbs_read_plus_write']:.1f} GB/s read+write")
     floor = bench_floor(qmm, hipr, stream, args.steps, args.warmup, g["alg_bytes_per_step"])
     log(f"read-only floor {floor['bytes']} B: {floor['us']:.2f} us ({floor['gbs']:.1f} GB/s)")
+    # the same floor for every other GEMV leg, over that leg's algorithmic bytes
+    floors = {g["alg_bytes_per_step"]: floor}
+    for rec in batched + shapes + kquant + [{"alg_bytes_per_step": down["alg_bytes_per_step"]}]:
+        nb = rec["alg_bytes_per_step"]
+        if nb not in floors:
+            floors[nb] = bench_floor(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), nb)
+            log(f"read-only floor {floors[nb]['bytes']} B: {floors[nb]['us']:.2f} us")
+        if "kernel_us" in rec:
+            rec["floor_us"] = round(floors[nb]["us"], 3)
+            rec["frac_of_floor"] = round(floors[nb]["us"] / rec["kernel_us"], 4)
+    down_floor = floors[down["alg_bytes_per_step"]]["us"]
     cpu = None if args.no_cpu else cpu_baseline(g, args.cpu_seconds)
 
     achieved = g["gbs_kernel"]
@@ -556,7 +567,8 @@ def main(argv=None) -> int:
         "pct_of_hbm_peak_wall": round(100.0 * g["gbs_wall"] / HBM_PEAK_GBS, 2),
         "down_proj": {"workload": "q4_0_gemv_n4096_k11008_b1", "value": round(down["gbs_wall"], 2),
                       "unit": "GB/s", "kernel_gbs": round(down["gbs_kernel"], 2),
-                      "kernel_us": round(down["kernel_ms"] * 1e3, 3), "sha256": down["sha256"]},
+                      "kernel_us": round(down["kernel_ms"] * 1e3, 3), "floor_us": round(down_floor, 3),
+                      "frac_of_floor": round(down_floor / (down["kernel_ms"] * 1e3), 4), "sha256": down["sha256"]},
         "cpu_baseline": cpu,
     }
     if copy:

@@ -99,10 +99,18 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
     if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
-// K-quant super-blocks -> chunks (layouts in qmm_internal.hpp).  One thread per chunk
-// slot, consecutive threads consecutive slots of a chunk, so a wave writes a chunk's
-// codes as one contiguous span; every byte of the chunk array is written (padding
-// rows as zeros).  Super-block reading as the reference's (paths relative to
+// K-quant super-blocks -> chunks (layouts in qmm_internal.hpp).  A workgroup fills the
+// kRepackChunks consecutive chunks of one row tile that cover two super-blocks (groups
+// 4q .. 4q + 3; a group is half a super-block); thread t fills slot t % 64 of chunk
+// t / 64, consecutive threads consecutive slots, so a wave writes a chunk's codes as one
+// contiguous span; every byte of the chunk array is written (padding rows as zeros).
+// Q6_K: a slot's 28 source bytes lie in three places of its super-block, so the 16 rows'
+// two super-blocks are first copied to LDS with coalesced 4-byte loads.  A row's span
+// may start at any byte: the loads run 4-byte aligned from a buffer resource based at
+// the source rounded down to 4 bytes, the source's last word is read byte by byte, and
+// nothing past the source is read.  Q4_K: a slot's 19 bytes are read straight from HBM
+// (measured faster than staging at 11008 x 4096: 16 vs 19 us; Q6_K staged 27 us, direct
+// 133-152 us).  Super-block reading as the reference's (paths relative to
 // openmini-server/src/model/inference/):
 //   Q4_K quant.rs:338-410: d = fp16 at 0, dmin = fp16 at 2, scale of sub-block sb =
 //        byte 4 + sb & 0x3F, codes from byte 12 (sub-block sb: 16 bytes at 12 + 16 sb,
@@ -111,30 +119,67 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
 //        (even i: low nibble), high = bits 2 (i % 4) of byte 66 + i / 4,
 //        q = low + 16 high - 32, scale = int8 byte 130 + i / 16.
 template <int kType>
-__global__ __launch_bounds__(256) void repack_kquant_kernel(const uint8_t* __restrict__ gguf, int64_t n,
-                                                            int64_t supers, int64_t groups, int64_t slots,
-                                                            uint8_t* __restrict__ chunks) {
+__global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uint8_t* __restrict__ gguf,
+                                                                       uint32_t src_bytes, int64_t n,
+                                                                       int64_t supers, int64_t groups,
+                                                                       int64_t quads,
+                                                                       uint8_t* __restrict__ chunks) {
     constexpr bool kQ6 = kType == OPENMINI_QMM_Q6_K;
     constexpr int kBPB = kQ6 ? 210 : 144;
     constexpr int kChunk = kQ6 ? kQ6KChunk : kQ4KChunk;
     constexpr int kScaleOff = kQ6 ? kTileEntries * 24 : kTileEntries * 16;
     constexpr int kDOff = kScaleOff + (kQ6 ? 2 : 1) * kTileEntries;
-    const int64_t gs = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gs >= slots) return;
-    const int64_t c = gs / kTileEntries;
-    const int e = (int)(gs % kTileEntries), r = e & 15, t = e >> 4;
-    const int64_t rt = c / groups, g = c % groups;
-    const int64_t row = rt * kTileRows + r;
-    const int sub = (int)(g & 1) * kTileBlocks + t;  // 32-element sub-block of super-block g / 2
-    uint8_t* ch = chunks + c * kChunk;
+    constexpr int kSpan = 2 * kBPB;                // one row's bytes in the workgroup
+    constexpr int kRowDw = (kSpan + 3 + 3) / 4;    // dwords that cover it from any start
+    static_assert(kRepackChunks == 4, "a workgroup covers two super-blocks");
+    __shared__ uint32_t stage[kQ6 ? kTileRows * kRowDw : 1];
+
+    const int64_t rt = (int64_t)blockIdx.x / quads, q = (int64_t)blockIdx.x % quads;
+    const int64_t row0 = rt * kTileRows, s0 = 2 * q;
+    const uint32_t delta = (uint32_t)((uintptr_t)gguf & 3u);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(gguf - delta), (short)0, (int)(src_bytes + delta), 0x00020000);
+    // byte offset of row r's span from the aligned base (fits: src_bytes + 3 < 2^32)
+    auto span_off = [&](int r) {
+        return (uint32_t)(((row0 + r) * supers + s0) * kBPB) + delta;
+    };
+    for (int i = threadIdx.x; kQ6 && i < kTileRows * kRowDw; i += kRepackThreads) {
+        const int r = i / kRowDw, j = i % kRowDw;
+        uint32_t v = 0;
+        if (row0 + r < n) {
+            const uint64_t a = (uint64_t)(span_off(r) & ~3u) + 4u * (uint32_t)j;
+            const uint64_t end = (uint64_t)src_bytes + delta;
+            if (a + 4 <= end) {
+                v = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)a, 0, 0);
+            } else {  // the source's last word may be partial: its bytes one by one
+#pragma unroll
+                for (uint32_t b = 0; b < 4; ++b)
+                    if (a + b < end)
+                        v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)(a + b), 0, 0) << (8 * b);
+            }
+        }
+        stage[i] = v;
+    }
+    if constexpr (kQ6) __syncthreads();
+
+    const int t = threadIdx.x, c = t / kTileEntries, e = t % kTileEntries, r = e & 15;
+    const int64_t g = q * kRepackChunks + c;
+    if (g >= groups) return;
+    const int64_t row = row0 + r;
+    const int sub = (c & 1) * kTileBlocks + (e >> 4);  // 32-element sub-block of super-block s0 + c / 2
+    uint8_t* ch = chunks + (rt * groups + g) * kChunk;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
     uint32_t sc = 0;
     uint16_t dbits = 0;
     if (row < n) {
-        const uint8_t* blk = gguf + (row * supers + (g >> 1)) * kBPB;
+        const uint8_t* blk =
+            kQ6 ? reinterpret_cast<const uint8_t*>(stage) + r * kRowDw * 4 + (span_off(r) & 3u) + (c >> 1) * kBPB
+                : gguf + (row * supers + s0 + (c >> 1)) * kBPB;
         const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
         if constexpr (!kQ6) {
-            const uint8_t* qs = blk + 12 + sub * 16;
+            uint8_t qs[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) qs[i] = blk[12 + sub * 16 + i];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 uint32_t v = 0;
@@ -148,15 +193,17 @@ __global__ __launch_bounds__(256) void repack_kquant_kernel(const uint8_t* __res
             const uint16_t dmin = (uint16_t)(blk[2] | (blk[3] << 8));
             dbits = (dmin & 0x7C00u) == 0x7C00u ? (uint16_t)0x7E00u : d;
         } else {
-            const uint8_t* ql = blk + 2;
-            const uint8_t* qh = blk + 66;
+            uint8_t ql[16], qh[8];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ql[i] = blk[2 + sub * 16 + i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qh[i] = blk[66 + sub * 8 + i];
             uint32_t lo4[32], hi2[32];
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                const int el = sub * 32 + i;
-                lo4[i] = (el & 1) ? (ql[el >> 1] >> 4) : (ql[el >> 1] & 0x0Fu);
+                lo4[i] = (i & 1) ? (ql[i >> 1] >> 4) : (ql[i >> 1] & 0x0Fu);
                 // v = q & 63 = low + 16 ((high + 2) & 3): the top bits are high ^ 2
-                hi2[i] = ((qh[el >> 2] >> ((el & 3) * 2)) & 3u) ^ 2u;
+                hi2[i] = ((qh[i >> 2] >> ((i & 3) * 2)) & 3u) ^ 2u;
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -186,7 +233,7 @@ __global__ __launch_bounds__(256) void repack_kquant_kernel(const uint8_t* __res
         reinterpret_cast<uint2*>(ch + kTileEntries * 16)[e] = make_uint2(w[4], w[5]);
         reinterpret_cast<uint16_t*>(ch + kScaleOff)[e] = (uint16_t)sc;
     }
-    if (t == 0) reinterpret_cast<uint16_t*>(ch + kDOff)[r] = dbits;
+    if ((e >> 4) == 0) reinterpret_cast<uint16_t*>(ch + kDOff)[r] = dbits;
 }
 
 // Chunked weight -> f32 [n][k] (8 * nwords outputs, row-major; one code word = 8
@@ -520,14 +567,18 @@ inline unsigned grid_for(int64_t items, int per_block) {
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
     if (w.n_tiles <= 0 || w.groups <= 0) return hipSuccess;
     if (is_kquant(w.type)) {
-        const int64_t slots = w.n_tiles * w.groups * kTileEntries;
-        const dim3 grid((unsigned)((slots + 255) / 256));
+        const int64_t supers = w.k / 256;
+        const int64_t src = w.n * supers * bytes_per_block(w.type);
+        // 32-bit buffer offsets: the source is smaller than the chunk array (< 4 GiB)
+        if (src + 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
+        const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
+        const dim3 grid((unsigned)(w.n_tiles * quads));
         if (w.type == OPENMINI_QMM_Q4_K)
-            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q4_K>, grid, dim3(256), 0, s, gguf, w.n, w.k / 256,
-                               w.groups, slots, w.chunks);
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q4_K>, grid, dim3(kRepackThreads), 0, s, gguf,
+                               (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
         else
-            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q6_K>, grid, dim3(256), 0, s, gguf, w.n, w.k / 256,
-                               w.groups, slots, w.chunks);
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q6_K>, grid, dim3(kRepackThreads), 0, s, gguf,
+                               (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
         return hipGetLastError();
     }
     const int aligned = ((uintptr_t)gguf % 16) == 0 && w.nb % 8 == 0;

@@ -126,6 +126,31 @@ def test_kquant_from_gguf_file(qmm, tmp_path, qtype):
     assert np.array_equal(gemv_nan_filled(qmm, w_file, x), gemv_nan_filled(qmm, w_direct, x))
 
 
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("offset", [0, 1, 2, 3, 6])
+def test_kquant_upload_from_device_any_alignment(qmm, orc, qtype, offset):
+    """Repack from super-blocks already in HBM at any byte offset.  The repack copies
+    each row's span to LDS in 4-byte words read from the source rounded down to 4
+    bytes, and the source's last word may be partial; the bytes around the source are
+    0xA5 here, so any byte read from outside it would change the result.  An odd
+    super-block count and a ragged last row tile; the GEMV equals the host-uploaded
+    weight's bit for bit and the oracle within tolerance."""
+    N, K = 37, 256 * 9
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC700 + offset)
+    staged = np.full(blocks.size + 16, 0xA5, dtype=np.uint8)
+    staged[offset: offset + blocks.size] = blocks
+    dbuf = qmm.DeviceBuffer.from_numpy(staged)
+    view = qmm.DeviceBuffer.__new__(qmm.DeviceBuffer)
+    view.nbytes, view.ptr = blocks.size, ctypes.c_void_p(dbuf.ptr.value + offset)
+    w_dev = qmm.QuantizedWeight.from_device(qtype, view, blocks.size, N, K)
+    view.ptr = ctypes.c_void_p()  # not owned
+    w_host = qmm.QuantizedWeight(qtype, blocks, N, K)
+    x = synth.normal(0xC701, (2, K), 1.0)
+    y = gemv_nan_filled(qmm, w_dev, x)
+    assert np.array_equal(y.view(np.uint32), gemv_nan_filled(qmm, w_host, x).view(np.uint32))
+    assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x), TOL, f"offset {offset}")
+
+
 def test_kquant_error_paths(qmm):
     L = _native.lib()
     blocks = synth.kquant_blocks(Q4_K, 16, 512, seed=0xC600)
