@@ -124,7 +124,8 @@ def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed
 
 def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q8_0, seed=0x5EED0003):
     from openmini_qmm import synth
-    blocks = synth.weight_blocks(qtype, N, K, seed=seed)
+    blocks = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
+              else synth.weight_blocks(qtype, N, K, seed=seed))
     copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // blocks.size))
     log(f"gemm type={qtype} N={N} K={K} M={M}: {copies} weight copies")
     ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
@@ -469,6 +470,14 @@ def main(argv=None) -> int:
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                             "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
             log(f"q8_0 gemm M={m}: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
+        # prefill on K-quant weights (Llama-7B up projection, M = 512)
+        for qtype in (Q4_K, Q6_K):
+            r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 8), max(3, args.warmup // 4), qtype=qtype,
+                           seed=0x5EED0081 + qtype)
+            prefill.append({"workload": f"{TYPE_NAME[qtype]}_gemm_n11008_k4096_m512_bf16x", "unit": "TFLOP/s",
+                            "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
+            log(f"{TYPE_NAME[qtype]} gemm M=512: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
     layer = None
     if not args.no_layer:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))

@@ -54,9 +54,9 @@ typedef enum {
     OPENMINI_QMM_ERR_NOT_FOUND = -12     /* "Tensor not found" / missing metadata key */
 } openmini_qmm_status_t;
 
-/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload and the
- * decode GEMV take Q4_0, Q8_0, Q4_K and Q6_K; the prefill GEMM takes Q4_0 and Q8_0; the
- * dequantization entry points take every id listed. */
+/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload, the
+ * decode GEMV and the prefill GEMM take Q4_0, Q8_0, Q4_K and Q6_K; the dequantization
+ * entry points take every id listed. */
 typedef enum {
     OPENMINI_QMM_F32 = 0,
     OPENMINI_QMM_F16 = 1,
@@ -130,8 +130,8 @@ size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
  * (gguf.rs:2062-2110) -> quant::dequantize (quant.rs:56).  Takes the tensor's raw
  * GGUF blocks (row n = k_cols/32 consecutive blocks, ggml ne0 = K), keeps them
  * quantized and repacks them on the GPU for its access pattern.
- * Types: Q4_0 and Q8_0 (GEMV and GEMM), Q4_K and Q6_K (GEMV; with the reference's own
- * reading of those blocks, quant.rs:338-410 and :515-600, whose values are exact
+ * Types: Q4_0, Q8_0, Q4_K and Q6_K (GEMV and GEMM; Q4_K / Q6_K with the reference's
+ * own reading of those blocks, quant.rs:338-410 and :515-600, whose values are exact
  * products of an integer code and an fp32 sub-block factor).
  * Errors: INVALID_PARAM (k_cols % 32, or % 256 for Q4_K / Q6_K; sizes <= 0),
  * UNSUPPORTED (type), INSUFFICIENT_DATA (gguf_bytes < required). */
@@ -164,7 +164,8 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
 
 /* Prefill GEMM: y[m, N] = x[m, K] . W^T with bf16 activations (raw bf16 bits),
  * fp32 output, on bf16 MFMA with exact integer codes and fp32 per-block scales.
- * Q4_0 and Q8_0 weights (UNSUPPORTED for Q4_K / Q6_K).  d_x must be 16-byte aligned. */
+ * Q4_0, Q8_0, Q4_K and Q6_K weights (Q6_K: code * 16-element scale, an exact integer,
+ * as two bf16 parts, then the fp32 d).  d_x must be 16-byte aligned. */
 int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
                            int64_t m, void* stream);
 

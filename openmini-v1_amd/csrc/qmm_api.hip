@@ -65,11 +65,12 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
-// Weight layouts of the upload and the decode GEMV; the GEMM takes Q4_0 and Q8_0.
+// Weight layouts of the upload, the decode GEMV and the prefill GEMM; dequant_weight
+// takes Q4_0 and Q8_0.
 bool type_supported(int type) {
     return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0 || qmm::is_kquant(type);
 }
-bool gemm_type(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
+bool plain_type(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
 // quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
 bool safe_type(int type) {
     return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0 || type == OPENMINI_QMM_Q4_1;
@@ -413,9 +414,6 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
-    if (!gemm_type(weight->w.type))
-        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "the prefill GEMM takes Q4_0 and Q8_0 weights, not type %d",
-                    weight->w.type);
     hipError_t e = qmm::launch_gemm_bf16(weight->w, d_x, d_y, m, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return ok();
@@ -491,9 +489,6 @@ int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini
     if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
-    if (!gemm_type(gate->w.type))
-        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "the prefill GEMM takes Q4_0 and Q8_0 weights, not type %d",
-                    gate->w.type);
     hipError_t e = qmm::launch_gemm_bf16(gate->w, d_x, d_h, m, as_stream(stream), false);
     if (e == hipSuccess) e = qmm::launch_gemm_bf16(up->w, d_x, d_h, m, as_stream(stream), true);
     if (e != hipSuccess) return hip_fail(e, "ffn_gate_up_bf16 launch");
@@ -555,7 +550,7 @@ int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, 
     if (rc != OPENMINI_QMM_OK) return rc;
     if (!d_out) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out");
     if (!aligned16(d_out)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "out must be 16-byte aligned");
-    if (!gemm_type(weight->w.type))
+    if (!plain_type(weight->w.type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
                     "dequant_weight takes Q4_0 and Q8_0 weights (K-quant bytes: openmini_qmm_dequantize_any_device)");
     hipError_t e = qmm::launch_dequant_weight(weight->w, d_out, as_stream(stream));

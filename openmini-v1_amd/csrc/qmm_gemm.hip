@@ -11,6 +11,11 @@
 // per-block rescale costs 4 VALU FMAs per MFMA, about as many VALU cycles as the
 // MFMA takes, so the kernel keeps both busy: two waves per SIMD, MFMA results in
 // VGPRs, and each MFMA issued before the FMAs of the previous one.
+// K-quant weights (the reference's reading, quant.rs:338-410 and :515-600) use their
+// 32-element sub-blocks as the blocks.  Q4_K: codes as Q4_0, block factor
+// 16 * d * scale (exact).  Q6_K: its scale changes every 16 elements, inside one
+// MFMA's 32, so q * scale (an exact integer of at most 13 bits) enters as bf16
+// hi + lo (two chained MFMAs, both exact), and the row's d is the block factor.
 //
 // Tiling: a workgroup computes a kBM x (48 kNW) tile of y with kNW column slices x
 // kKS K parts of waves (launch_kind picks 128 x 96 with 2 x 2 waves, or 64 x 96
@@ -75,13 +80,63 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// A wave's weight operands for one K step: per weight tile j and block tt of the
-// step, the lane's 8 codes (two words Q8_0 / one word Q4_0) and its column's scale.
-template <bool kQ4, int kSB>
-struct BRegs {
-    uint32_t c[kWT][kSB][kQ4 ? 1 : 2];
-    uint32_t s[kWT][kSB];
+// Chunk geometry the GEMM reads, by weight format (layouts in qmm_internal.hpp).
+template <int kFmt>
+struct GFmt {
+    static constexpr bool kQ8 = kFmt == OPENMINI_QMM_Q8_0;
+    static constexpr bool kQ4K = kFmt == OPENMINI_QMM_Q4_K;
+    static constexpr bool kQ6K = kFmt == OPENMINI_QMM_Q6_K;
+    static constexpr bool kKQ = kQ4K || kQ6K;
+    static constexpr bool kNib = !kQ8 && !kQ6K;            // Q4_0 / Q4_K: 16 B of nibbles per slot
+    static constexpr int kCB = kQ8 ? 32 : 16;               // bytes of a slot's (low) codes
+    static constexpr int kWords = kNib ? 1 : 2;             // code words per lane and block
+    static constexpr int kScaleOff = kTileEntries * (kQ6K ? 24 : kCB);
+    static constexpr int kDOff = kScaleOff + (kQ6K ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
+    static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ6K ? kQ6KChunk : chunk_bytes_for(!kQ8);
+    // buffer loads one load_b issues per (tile, block), plus the K-quant d per tile
+    static constexpr int kLoadsPerBlock = kQ6K ? 3 : 2;
+    static constexpr int kLoadsPerTile = kKQ ? 1 : 0;
 };
+
+// A wave's weight operands for one K step: per weight tile j and block tt of the
+// step, the lane's 8 codes (Q4_0 / Q4_K one word of nibbles, Q8_0 two words of
+// bytes, Q6_K the low-nibble word and the top-bit word), its column's scale, and for
+// K-quants the column's d (one per step: a step stays inside one group).
+template <int kFmt, int kSB>
+struct BRegs {
+    uint32_t c[kWT][kSB][GFmt<kFmt>::kWords];
+    uint32_t s[kWT][kSB];
+    uint32_t d[kWT];
+};
+
+// 8 Q6_K codes of lane quarter kq -> bf16 hi / lo parts of q * sc, q * sc exact (at
+// most 13 significant bits): hi keeps the top 8 bits, lo = q * sc - hi has at most 5.
+// w: the slot's low-nibble word kq; hm: its top-bit word kq / 2 (qmm_internal.hpp).
+__device__ __forceinline__ void split_q6(uint32_t w, uint32_t hm, int kq, float sc4, bf16x8& hi, bf16x8& lo) {
+    // 4 q per int8 byte: low 4 bits at 2..5, the top 2 bits (fields 2 (kq & 1) and
+    // 2 (kq & 1) + 1 of each byte of hm) at 6..7; elements 8 kq + 0..3, then + 4..7
+    const int sh = (kq & 1) * 4;
+    const uint32_t b0 = ((w << 2) & 0x3C3C3C3Cu) | ((hm << (6 - sh)) & 0xC0C0C0C0u);
+    const uint32_t b1 = ((w >> 2) & 0x3C3C3C3Cu) | ((hm << (4 - sh)) & 0xC0C0C0C0u);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // (4 q) * (sc / 4): exact
+        f[i] = (float)(int8_t)((b0 >> (8 * i)) & 0xFFu) * sc4;
+        f[4 + i] = (float)(int8_t)((b1 >> (8 * i)) & 0xFFu) * sc4;
+    }
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t u0 = __float_as_uint(f[2 * p]), u1 = __float_as_uint(f[2 * p + 1]);
+        const float r0 = f[2 * p] - __uint_as_float(u0 & 0xFFFF0000u);
+        const float r1 = f[2 * p + 1] - __uint_as_float(u1 & 0xFFFF0000u);
+        h[p] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+        l[p] = pack_hi16(r0, r1);
+    }
+    hi = __builtin_bit_cast(bf16x8, *reinterpret_cast<uint4*>(h));
+    lo = __builtin_bit_cast(bf16x8, *reinterpret_cast<uint4*>(l));
+}
 
 // s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
@@ -106,14 +161,15 @@ struct Shape {
 
 // kGate: y holds the gate projection on entry and each element is replaced by
 // silu(gate) * (x . W^T), silu(v) = v / (1 + exp(-v)) (model.rs:713-735, :1187-1189).
-template <bool kQ4, int kBM, int kNW, int kKS, int kSB, bool kGate>
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate>
 __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ chunks, float* __restrict__ y,
     int m_rows, int n_rows, int n_tiles, int groups, int k) {
     using S = Shape<kBM, kNW, kKS, kSB>;
+    using F = GFmt<kFmt>;
     constexpr int kMI = S::kMI;
-    constexpr int kCB = kQ4 ? 16 : 32;
-    constexpr int kChunk = chunk_bytes_for(kQ4);
+    constexpr int kCB = F::kCB;
+    constexpr int kChunk = F::kChunk;
     constexpr int kStepsPerGroup = kTileBlocks / kSB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLdsB];
 
@@ -160,17 +216,27 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     uint32_t tile_off[kWT];
 #pragma unroll
     for (int j = 0; j < kWT; ++j) tile_off[j] = (uint32_t)min(tile0 + j, n_tiles - 1) * groups * kChunk;
-    auto load_b = [&](BRegs<kQ4, kSB>& B, int u) {
+    auto load_b = [&](BRegs<kFmt, kSB>& B, int u) {
         const int g = u / kStepsPerGroup, t0 = (u % kStepsPerGroup) * kSB;
 #pragma unroll
         for (int j = 0; j < kWT; ++j) {
             const uint32_t soff = tile_off[j] + (uint32_t)g * kChunk;
+            if constexpr (F::kKQ) B.d[j] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, F::kDOff + li * 2, soff, 0);
 #pragma unroll
             for (int tt = 0; tt < kSB; ++tt) {
                 const uint32_t slot = (uint32_t)((t0 + tt) * kTileRows + li);
-                B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, kTileEntries * kCB + slot * 2, soff, 0);
-                if constexpr (kQ4) {
+                if constexpr (F::kQ4K)
+                    B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b8(w_rs, F::kScaleOff + slot, soff, 0);
+                else if constexpr (F::kQ6K)  // the scale of the lane's 16-element half
+                    B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b8(w_rs, F::kScaleOff + slot * 2 + (kq >> 1), soff, 0);
+                else
+                    B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, F::kScaleOff + slot * 2, soff, 0);
+                if constexpr (F::kNib) {
                     B.c[j][tt][0] = __builtin_amdgcn_raw_buffer_load_b32(w_rs, slot * kCB + kq * 4, soff, 0);
+                } else if constexpr (F::kQ6K) {
+                    B.c[j][tt][0] = __builtin_amdgcn_raw_buffer_load_b32(w_rs, slot * kCB + kq * 4, soff, 0);
+                    B.c[j][tt][1] = __builtin_amdgcn_raw_buffer_load_b32(
+                        w_rs, kTileEntries * 16 + slot * 8 + (kq >> 1) * 4, soff, 0);
                 } else {
                     const uint2 v = __builtin_bit_cast(
                         uint2, __builtin_amdgcn_raw_buffer_load_b64(w_rs, slot * kCB + kq * 8, soff, 0));
@@ -199,14 +265,50 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
                                                   slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16)));
         }
     };
+    // Q6_K block tt: the scale changes every 16 elements, inside an MFMA's 32, so it is
+    // folded into the codes: q * sc (exact integers) as bf16 hi + lo, two chained MFMAs
+    // per subtile, then one FMA per output with the row's d.
+    auto compute_q6 = [&](const BRegs<kFmt, kSB>& B, const AFrags& a, int tt) {
+        if constexpr (F::kQ6K) {
+            bf16x8 bh[kWT], bl[kWT];
+            float d[kWT];
+#pragma unroll
+            for (int j = 0; j < kWT; ++j) {
+                split_q6(B.c[j][tt][0], B.c[j][tt][1], kq, (float)(int8_t)(B.s[j][tt] & 0xFFu) * 0.25f, bh[j], bl[j]);
+                d[j] = f16_bits_to_f32((uint16_t)B.d[j]);
+            }
+            f32x4 pp[2];
+            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bh[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bl[0], pp[0], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kMI * kWT; ++q) {
+                if (q + 1 < kMI * kWT) {
+                    const int i1 = (q + 1) / kWT, j1 = (q + 1) % kWT;
+                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i1], bh[j1], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                               0, 0, 0);
+                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i1], bl[j1], pp[(q + 1) & 1], 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
+            }
+        }
+    };
     // Block tt of one step: 8 x 3 MFMAs on A fragments `a` and the weight registers.
-    auto compute = [&](const BRegs<kQ4, kSB>& B, const AFrags& a, int tt) {
+    auto compute = [&](const BRegs<kFmt, kSB>& B, const AFrags& a, int tt) {
+        if constexpr (F::kQ6K) {
+            compute_q6(B, a, tt);
+            return;
+        }
         bf16x8 b[kWT];
         float d[kWT];
 #pragma unroll
         for (int j = 0; j < kWT; ++j) {
             const uint16_t dh = (uint16_t)B.s[j][tt];
-            if constexpr (kQ4) {
+            if constexpr (F::kQ4K) {  // (q - 8) / 16 codes; block factor 16 d * scale (exact)
+                b[j] = cvt_q4(B.c[j][tt][0]);
+                d[j] = f16_bits_to_f32((uint16_t)B.d[j]) * (float)(B.s[j][tt] & 0xFFu) * 16.0f;
+            } else if constexpr (F::kNib) {
                 b[j] = cvt_q4(B.c[j][tt][0]);
                 d[j] = f16_bits_to_f32(dh) * 16.0f;
             } else {
@@ -236,9 +338,10 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     // unconditional (units past this part's end re-load its last unit, a cache hit)
     // so the count of outstanding loads is the same on every path; the compiler's
     // own waits before the barrier then cover only the x copies.
-    constexpr int kBLoads = kWT * kSB * 2;
+    constexpr int kBLoads = kWT * (kSB * F::kLoadsPerBlock + F::kLoadsPerTile);
+    static_assert(kBLoads <= 63, "vmcnt counts up to 63");
     const int u_last = max(u1 - 1, 0);
-    auto step = [&](int it, const BRegs<kQ4, kSB>& cur, BRegs<kQ4, kSB>& far) {
+    auto step = [&](int it, const BRegs<kFmt, kSB>& cur, BRegs<kFmt, kSB>& far) {
         const int u = u0 + it;
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
         __syncthreads();
@@ -265,7 +368,7 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
             }
     };
 
-    BRegs<kQ4, kSB> b0, b1, b2;
+    BRegs<kFmt, kSB> b0, b1, b2;
     issue_x(min(u0, u_last), 0);
     asm volatile("" ::: "memory");
     load_b(b0, min(u0, u_last));
@@ -323,12 +426,12 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     }
 }
 
-template <bool kQ4, int kBM, int kNW, int kKS, int kSB, bool kGate>
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate>
 hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
     using S = Shape<kBM, kNW, kKS, kSB>;
     const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL((gemm_kernel<kQ4, kBM, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks, y,
-                       (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+    hipLaunchKernelGGL((gemm_kernel<kFmt, kBM, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks,
+                       y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
     return hipGetLastError();
 }
 
@@ -339,10 +442,21 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m,
 // overlap the other's work).  Measured on MI355X, Q8_0 11008 x 4096: M = 128 29.8 us
 // (128 x 48 tiles with 4 K parts: 35.6 us); M = 256 / 512 / 2048 against 64-row tiles
 // and 4 x 2 (128 x 192) tiles: equal or faster.
-template <bool kQ4, bool kGate>
+template <int kFmt, bool kGate>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
-    if (m <= kBMMax) return launch_shape<kQ4, 64, 2, 4, 2, kGate>(w, x, y, m, s);
-    return launch_shape<kQ4, 128, 2, 2, 2, kGate>(w, x, y, m, s);
+    if (m <= kBMMax) return launch_shape<kFmt, 64, 2, 4, 2, kGate>(w, x, y, m, s);
+    return launch_shape<kFmt, 128, 2, 2, 2, kGate>(w, x, y, m, s);
+}
+
+template <bool kGate>
+hipError_t launch_type(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
+    switch (w.type) {
+    case OPENMINI_QMM_Q4_0: return launch_kind<OPENMINI_QMM_Q4_0, kGate>(w, x, y, m, s);
+    case OPENMINI_QMM_Q8_0: return launch_kind<OPENMINI_QMM_Q8_0, kGate>(w, x, y, m, s);
+    case OPENMINI_QMM_Q4_K: return launch_kind<OPENMINI_QMM_Q4_K, kGate>(w, x, y, m, s);
+    case OPENMINI_QMM_Q6_K: return launch_kind<OPENMINI_QMM_Q6_K, kGate>(w, x, y, m, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -356,11 +470,8 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
         const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
         const uint16_t* xs = x + m_off * w.k;
         float* ys = y + m_off * w.n;
-        const bool q4 = w.type == OPENMINI_QMM_Q4_0;
-        const hipError_t e = gate_in_y ? (q4 ? launch_kind<true, true>(w, xs, ys, mm, s)
-                                             : launch_kind<false, true>(w, xs, ys, mm, s))
-                                       : (q4 ? launch_kind<true, false>(w, xs, ys, mm, s)
-                                             : launch_kind<false, false>(w, xs, ys, mm, s));
+        const hipError_t e =
+            gate_in_y ? launch_type<true>(w, xs, ys, mm, s) : launch_type<false>(w, xs, ys, mm, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -27,8 +27,9 @@
 // 8j..8j+3 and 8j+4..8j+7 as int8 bytes, in order (ready-made int8 MFMA operands),
 // and v_cvt_off_f32_i4 turns a nibble into (q - 8) / 16 in one op.
 //
-// K-quant weights (decode GEMV only) use the same tiles with 32-element sub-blocks as
-// the "blocks" (a 256-element super-block = 8 sub-blocks = 2 groups, so K % 256 == 0):
+// K-quant weights (decode GEMV and prefill GEMM) use the same tiles with 32-element
+// sub-blocks as the "blocks" (a 256-element super-block = 8 sub-blocks = 2 groups,
+// so K % 256 == 0):
 //   Q4_K (144-byte super-blocks, reference reading quant.rs:338-410): element value
 //     (q - 8) * d * scale + dmin * 0 (the reference's minimum is always 0); both
 //     products are exact, so the value is (q - 8) * (d * scale).  Slot codes as Q4_0

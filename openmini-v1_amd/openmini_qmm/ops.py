@@ -28,8 +28,7 @@ QK = 32
 
 class GgufTensorType(enum.IntEnum):
     """GGUF type ids, model/inference/gguf.rs:219-240: the layouts this library
-    dequantizes (weights: Q4_0 and Q8_0 for the GEMV and GEMM, Q4_K and Q6_K for the
-    decode GEMV)."""
+    dequantizes (weights for the GEMV and GEMM: Q4_0, Q8_0, Q4_K and Q6_K)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
@@ -164,8 +163,8 @@ def init(device: int = 0) -> None:
 
 class QuantizedWeight:
     """A GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor W[n_rows, k_cols] uploaded and repacked in
-    HBM (the K-quants serve the decode GEMV; the prefill GEMM returns UNSUPPORTED for
-    them).
+    HBM, served by the decode GEMV and the prefill GEMM (dequantize() takes Q4_0 and
+    Q8_0 handles).
 
     Replaces QuantizedWeightLoader::load_tensor_data (quant_loader.rs:76-92), which
     dequantizes to f32 at load; here the raw blocks stay quantized on the GPU."""

@@ -163,6 +163,96 @@ def test_kquant_error_paths(qmm):
         == _native.ERR_INSUFFICIENT_DATA
     w = qmm.QuantizedWeight(Q4_K, blocks, 16, 512)
     assert w.info().gguf_bytes == 16 * 2 * 144
-    dx, dy = qmm.DeviceBuffer(16 * 512 * 2), qmm.DeviceBuffer(16 * 16 * 4)
-    assert L.openmini_qmm_gemm_bf16(w.handle, dx.ptr, dy.ptr, 16, None) == _native.ERR_UNSUPPORTED
+    dy = qmm.DeviceBuffer(16 * 512 * 4)
     assert L.openmini_qmm_dequant_weight(w.handle, dy.ptr, None) == _native.ERR_UNSUPPORTED
+
+
+def run_gemm(qmm, w, xb16):
+    M = xb16.shape[0]
+    dx = qmm.DeviceBuffer.from_numpy(np.ascontiguousarray(xb16))
+    dy = qmm.DeviceBuffer(M * w.n_rows * 4)
+    dy.fill(0xFF)  # NaN: an output the kernel does not write fails the check
+    w.gemm_bf16(dx, dy, M)
+    return dy.download(np.float32, (M, w.n_rows))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K,M", [(16, 256, 1), (37, 512, 5), (130, 2304, 130), (300, 4096, 200),
+                                   (257, 1024, 384)])
+def test_kquant_gemm_parity(qmm, orc, qtype, N, K, M):
+    """Prefill GEMM on K-quant weights (bf16 x): both tile shapes (M <= 128 and
+    above), ragged row tiles, an odd super-block count, against the fp64 oracle over
+    the reference's element values."""
+    print(f"kquant gemm type={qtype} N={N} K={K} M={M}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC800 + N + K + M)
+    xb = synth.to_bf16_bits(synth.normal(0xC801 + M, (M, K), 1.0))
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    assert_parity(run_gemm(qmm, w, xb), orc.linear_bf16x_f64(qtype, blocks, N, K, xb), TOL, f"{N}x{K} M={M}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K,M", [(11008, 4096, 512), (4096, 11008, 128)])
+def test_kquant_gemm_llama_shapes_row_sample(qmm, orc, qtype, N, K, M):
+    """Llama-7B up / down projections at prefill sizes.  A row of y depends only on
+    its own x row, so the oracle runs on a sample of rows."""
+    print(f"kquant gemm full type={qtype} N={N} K={K} M={M}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xC900 + N + M)
+    xb = synth.to_bf16_bits(synth.normal(0xC901 + M, (M, K), 1.0))
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y = run_gemm(qmm, w, xb)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M + N).integers(0, M, 6)]))
+    print(assert_parity(y[rows], orc.linear_bf16x_f64(qtype, blocks, N, K, xb[rows]), TOL, "llama"))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("M", [4, 200])
+def test_kquant_gemm_one_hot_columns_exact(qmm, orc, qtype, M):
+    """x rows = e_k (bf16 1.0) make y[m] = W[:, k] exactly.  Q4_K: the code
+    (q - 8) / 16 times 16 d * scale is one exact product.  Q6_K: q * scale goes in as
+    bf16 hi + lo, whose MFMA sum is exact, and one rounding of (q * scale) * d equals
+    the reference's ((q * d) * scale) (q * d exact).  Columns at sub-block, half and
+    super-block edges."""
+    N, K = 77, 1024
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xCA00 + qtype)
+    W = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    cols = np.array([0, 15, 16, 31, 32, 255, 256, 511, 700, 1023])
+    cols = np.resize(cols, M)
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), cols] = 1.0
+    y = run_gemm(qmm, w, synth.to_bf16_bits(x))
+    for i, c in enumerate(cols):  # value equality: a zero weight may be -0.0 in the reference
+        assert np.array_equal(y[i], W[:, c]), (i, c, np.nonzero(y[i] != W[:, c]))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_gemm_matches_gemv(qmm, qtype):
+    """The GEMM and the decode GEMV are independent kernels; on the same
+    bf16-representable activations they agree to fp32 reassociation."""
+    N, K, M = 1000, 4096, 8
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xCB00 + qtype)
+    xb = synth.to_bf16_bits(synth.normal(0xCB01, (M, K), 1.0))
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y_mm = run_gemm(qmm, w, xb)
+    x32 = synth.bf16_bits_to_f32(xb).reshape(M, K)
+    y_mv = np.concatenate([gemv_nan_filled(qmm, w, x32[i:i + 4]) for i in range(0, M, 4)])
+    p = assert_parity(y_mm, y_mv.astype(np.float64), TOL, "gemm vs gemv")
+    assert p["normwise"] <= 2e-6, p
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K,M", [(1280, 512, 96), (11008, 4096, 256)])
+def test_kquant_ffn_gate_up_bf16(qmm, orc, qtype, N, K, M):
+    """Prefill FFN hidden state silu(x . Wg^T) * (x . Wu^T) through the GEMM's
+    SwiGLU epilogue on K-quant weights (oracle on a sample of rows at full size)."""
+    print(f"kquant ffn_gate_up_bf16 type={qtype} N={N} K={K} M={M}", flush=True)
+    bg, bu = synth.kquant_blocks(qtype, N, K, 0xCC00 + N), synth.kquant_blocks(qtype, N, K, 0xCC01 + N)
+    wg, wu = qmm.QuantizedWeight(qtype, bg, N, K), qmm.QuantizedWeight(qtype, bu, N, K)
+    xb = synth.to_bf16_bits(synth.normal(0xCC02 + M, (M, K), 1.0))
+    dx, dh = qmm.DeviceBuffer.from_numpy(xb), qmm.DeviceBuffer(M * N * 4)
+    qmm.ffn_gate_up_bf16(wg, wu, dx, dh, M)
+    h = dh.download(np.float32, (M, N))
+    rows = np.arange(M)
+    if M * N * K > (1 << 31):
+        rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M + N).integers(0, M, 6)]))
+    assert_parity(h[rows], orc.ffn_hidden_bf16x_f64(qtype, bg, bu, N, K, xb[rows]), TOL, "hidden bf16")
