@@ -24,6 +24,7 @@ import argparse
 import concurrent.futures as cf
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -177,6 +178,53 @@ def bench_floor(qmm, hipr, stream, steps, warmup, nbytes: int) -> dict:
     for b in bufs:
         b.free()
     return {"bytes": nbytes, "copies": copies, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9}
+
+
+def bench_ceiling(qmm, hipr, stream, steps, warmup, M, N=11008, K=4096, qtype=Q8_0) -> dict:
+    """The prefill GEMM's compute-only ceiling (openmini_qmm_gemm_ceiling): the GEMM's
+    grid and per-block register work for the same M x N x K, without memory traffic,
+    timed like the GEMM (graph replay, events on the stream)."""
+    sink = qmm.DeviceBuffer(256)
+    sh = stream.handle
+
+    def launch(i):
+        qmm.gemm_ceiling(qtype, M, N, K, sink, sh)
+
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    ms = time_steps(launch, steps, sh, hipr) / steps
+    sink.free()
+    return {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+
+
+def bench_dense_bf16(steps, warmup, M, N=11008, K=4096) -> dict:
+    """Yardstick: a dense bf16 GEMM of the same shape through torch.mm (hipBLASLt),
+    y_bf16[M, N] = x_bf16[M, K] . W_bf16[N, K]^T with fp32 accumulation: the weight
+    row-major [N, K] as the quantized kernels hold it (hipBLASLt's fastest layout for
+    this shape on MI355X, ahead of a [K, N] weight), dense bf16 (2 bytes per weight
+    against the quantized 0.56-1.06), rotated over >= 512 MB of copies, timed with
+    torch events over `steps` launches."""
+    import torch
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(0x5EED00B1)
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16).to(dev)
+    w = (torch.randn(N, K, generator=gen) * 0.02).to(torch.bfloat16)
+    copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // (w.numel() * 2)))
+    ws = [w.to(dev) for _ in range(copies)]
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    for i in range(warmup):
+        torch.mm(x, ws[i % copies].t(), out=y)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        torch.mm(x, ws[i % copies].t(), out=y)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    del ws
+    return {"M": M, "us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12, "weight_copies": copies}
 
 
 def copy_calibration(qmm, hipr, stream, reps: int = 5, nbytes: int = 256 << 20) -> dict:
@@ -435,6 +483,9 @@ def main(argv=None) -> int:
     ap.add_argument("--no-shapes", action="store_true", help="skip the other batch-1 decode shapes")
     ap.add_argument("--eager", action="store_true",
                     help="launch directly instead of replaying a HIP graph (for counter runs)")
+    ap.add_argument("--dense-bf16", action="store_true",
+                    help="also time a dense bf16 GEMM of the prefill shapes through torch (hipBLASLt)")
+    ap.add_argument("--dense-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run the streaming-copy yardstick kernel (for counter runs)")
     args = ap.parse_args(argv)
@@ -444,6 +495,23 @@ def main(argv=None) -> int:
         print(f"bench.py measures one GPU: this build targets a single MI355X and runs no "
               f"collectives (asked for --gpus {args.gpus})", file=sys.stderr)
         return 2
+
+    if args.dense_only:  # the child process of --dense-bf16: torch only, one JSON line
+        print(json.dumps([bench_dense_bf16(max(10, args.steps // 4), max(3, args.warmup // 4), m)
+                          for m in (128, 512, 2048)]), flush=True)
+        return 0
+    dense = []
+    if args.dense_bf16 and not args.no_gemm:
+        # torch carries its own HIP runtime: it runs in a child process started before
+        # this one touches the GPU, so the two runtimes never share a process
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--dense-only", "--steps", str(args.steps),
+                            "--warmup", str(args.warmup)], capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            print(r.stderr[-2000:], file=sys.stderr)
+            return r.returncode
+        dense = json.loads(r.stdout.strip().splitlines()[-1])
+        for d in dense:
+            log(f"dense bf16 torch.mm M={d['M']}: {d['us']:.2f} us, {d['tflops']:.1f} TFLOP/s")
 
     import openmini_qmm as qmm
     from openmini_qmm import hip_runtime as hipr
@@ -461,14 +529,19 @@ def main(argv=None) -> int:
     prefill = []
     if not args.no_gemm:
         gemm = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
+        gemm["ceiling"] = bench_ceiling(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), M=512)
         log(f"q8_0 gemm M=512: wall {gemm['tflops_wall']:.1f} TFLOP/s, kernel "
-            f"{gemm['tflops_kernel']:.1f} TFLOP/s")
+            f"{gemm['tflops_kernel']:.1f} TFLOP/s; compute-only ceiling {gemm['ceiling']['us']:.2f} us "
+            f"({gemm['ceiling']['tflops']:.1f} TFLOP/s)")
         # the other prefill sizes of BASELINE configs[3]
         for m in (128, 2048):
             r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 8), max(3, args.warmup // 4), M=m)
+            c = bench_ceiling(qmm, hipr, stream, max(10, args.steps // 8), max(3, args.warmup // 4), M=m)
             prefill.append({"workload": f"q8_0_gemm_n11008_k4096_m{m}_bf16x", "unit": "TFLOP/s",
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
-                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
+                            "ceiling_us": round(c["us"], 3), "frac_of_ceiling": round(c["us"] / (r["kernel_ms"] * 1e3), 4),
+                            "sha256": r["sha256"]})
             log(f"q8_0 gemm M={m}: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
         # prefill on K-quant weights (Llama-7B up projection, M = 512)
         for qtype in (Q4_K, Q6_K):
@@ -591,10 +664,20 @@ def main(argv=None) -> int:
             "roofline": {"bound": "mfma", "achieved": round(gemm["tflops_kernel"], 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                         "kernel_us": round(gemm["kernel_ms"] * 1e3, 3)},
+                         "kernel_us": round(gemm["kernel_ms"] * 1e3, 3),
+                         "ceiling_us": round(gemm["ceiling"]["us"], 3),
+                         "ceiling_tflops": round(gemm["ceiling"]["tflops"], 2),
+                         "frac_of_ceiling": round(gemm["ceiling"]["us"] / (gemm["kernel_ms"] * 1e3), 4),
+                         "ceiling": "openmini_qmm_gemm_ceiling: the same grid and per-block register work, "
+                                    "no memory traffic"},
         }
     if prefill:
         out["prefill_sizes"] = prefill
+    if dense:
+        out["gemm"]["yardstick_dense_bf16"] = {
+            "what": "torch.mm(x_bf16, W_bf16[N, K].t()) -> bf16 (hipBLASLt), dense bf16 weights of the same "
+                    "shape, rotated over >= 512 MB",
+            "legs": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in d.items()} for d in dense]}
     if batched:
         out["batched_decode"] = batched
     if shapes:

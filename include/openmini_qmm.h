@@ -369,10 +369,20 @@ int openmini_qmm_stream_copy(void* d_dst, const void* d_src, size_t bytes, void*
  * 16-byte aligned source) on `stream`, 16-byte loads, workgroups of 512 lanes over
  * consecutive 16 KB spans (the fastest read shape measured on MI355X).  Nothing is
  * written in practice; d_sink (4 bytes, 4-byte aligned) receives a word only if the
- * data fold hits a sentinel.  The time a
- * read-bound kernel of that many bytes cannot beat in one launch; the decode GEMV
- * is measured against it.  No counterpart in the reference. */
+ * data fold hits a sentinel.  The time a read-bound kernel of that many bytes cannot
+ * beat in one launch; the decode GEMV is measured against it.  No counterpart in the
+ * reference. */
 int openmini_qmm_stream_read(const void* d_src, size_t bytes, void* d_sink, void* stream);
+
+/* Compute-only ceiling of the prefill GEMM: for an m x n x k problem on a Q4_0 or
+ * Q8_0 weight (type), the grid and waves openmini_qmm_gemm_bf16 would launch, each
+ * running only its per-block register work (code conversion, MFMAs, rescale FMAs) on
+ * operands held in registers: no loads, LDS traffic, barriers or stores.  d_sink
+ * (4 bytes, 4-byte aligned) receives a word only if a sentinel is hit.  Its time is
+ * what the GEMM's instruction mix alone costs; the GEMM is measured against it.
+ * INVALID_PARAM for sizes <= 0, k % 32 != 0; UNSUPPORTED for other types.  No
+ * counterpart in the reference. */
+int openmini_qmm_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, void* d_sink, void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

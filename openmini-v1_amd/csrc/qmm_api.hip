@@ -791,4 +791,16 @@ int openmini_qmm_stream_read(const void* d_src, size_t bytes, void* d_sink, void
     return ok();
 }
 
+int openmini_qmm_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, void* d_sink, void* stream) {
+    if (!d_sink || ((uintptr_t)d_sink & 3u)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null or unaligned sink");
+    if (!plain_type(type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "gemm_ceiling takes Q4_0 and Q8_0, not type %d", type);
+    if (m <= 0 || n <= 0 || k <= 0 || k % 32 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "gemm_ceiling sizes m=%lld n=%lld k=%lld", (long long)m,
+                    (long long)n, (long long)k);
+    hipError_t e = qmm::launch_gemm_ceiling(type, m, n, k, static_cast<float*>(d_sink), as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemm_ceiling launch");
+    return ok();
+}
+
 }  // extern "C"

@@ -459,7 +459,95 @@ hipError_t launch_type(const Weight& w, const uint16_t* x, float* y, int64_t m, 
     }
 }
 
+// Compute-only ceiling of the prefill GEMM (Q4_0 / Q8_0): gemm_kernel's grid and
+// waves, each running only its per-block register work -- kWT code conversions,
+// kMI x kWT MFMAs and their rescale FMAs, in the same order -- for as many blocks as
+// its K part holds, on operands that stay in registers.  No loads, LDS, barriers or
+// stores (a sentinel store keeps the work live), so its time is what the GEMM's
+// instruction mix alone costs under the same clock and power conditions.
+template <int kFmt, int kMI>
+__global__ __launch_bounds__(512) void gemm_ceiling_kernel(int blocks, float* __restrict__ sink) {
+    constexpr bool kNib = kFmt == OPENMINI_QMM_Q4_0;
+    const int lane = threadIdx.x & 63;
+    bf16x8 a[kMI];
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[i][e] = (__bf16)((float)((lane + 7 * i + e) & 15) * 0.125f);
+    uint32_t c0[kWT], c1[kWT], sc[kWT];
+#pragma unroll
+    for (int j = 0; j < kWT; ++j) {
+        c0[j] = 0x01030507u * (uint32_t)(lane + j + 1);
+        c1[j] = 0x02040608u * (uint32_t)(lane + j + 1);
+        sc[j] = 0x3C00u;  // fp16 1.0
+    }
+    f32x4 acc[kMI][kWT];
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < blocks; ++b) {
+        // new operands every block, as the A-fragment reads and weight loads give
+#pragma unroll
+        for (int i = 0; i < kMI; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+        for (int j = 0; j < kWT; ++j) asm volatile("" : "+v"(c0[j]), "+v"(c1[j]), "+v"(sc[j]));
+        bf16x8 bq[kWT];
+        float d[kWT];
+#pragma unroll
+        for (int j = 0; j < kWT; ++j) {
+            if constexpr (kNib) {
+                bq[j] = cvt_q4(c0[j]);
+                d[j] = f16_bits_to_f32((uint16_t)sc[j]) * 16.0f;
+            } else {
+                bq[j] = cvt_q8(c0[j], c1[j]);
+                d[j] = f16_bits_to_f32((uint16_t)sc[j]);
+            }
+        }
+        f32x4 pp[2];
+        pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bq[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < kMI * kWT; ++q) {
+            if (q + 1 < kMI * kWT)
+                pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    a[(q + 1) / kWT], bq[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
+        }
+    }
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int j = 0; j < kWT; ++j) t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
+    if (t == 1234.5f) sink[0] = t;
+}
+
+template <int kFmt>
+hipError_t launch_ceiling(int64_t m, int64_t n_tiles, int64_t k, float* sink, hipStream_t s) {
+    // the grid, workgroup and K split of launch_kind's two shapes
+    const bool small = m <= kBMMax;
+    const int bm = small ? 64 : 128, threads = small ? 512 : 256, parts = small ? 4 : 2;
+    const int64_t bt = 2 * kWT;  // weight tiles per workgroup (2 column slices)
+    const dim3 grid((unsigned)((n_tiles + bt - 1) / bt), (unsigned)((m + bm - 1) / bm));
+    const int blocks = (int)((k / kQK + parts - 1) / parts);
+    if (small)
+        hipLaunchKernelGGL((gemm_ceiling_kernel<kFmt, 4>), grid, dim3(threads), 0, s, blocks, sink);
+    else
+        hipLaunchKernelGGL((gemm_ceiling_kernel<kFmt, 8>), grid, dim3(threads), 0, s, blocks, sink);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, float* sink, hipStream_t s) {
+    const int64_t n_tiles = (n + kTileRows - 1) / kTileRows;
+    if (m <= 0 || n <= 0 || k <= 0 || (m + 127) / 128 > 65535 || n_tiles > INT32_MAX) return hipErrorInvalidValue;
+    if (type == OPENMINI_QMM_Q4_0) return launch_ceiling<OPENMINI_QMM_Q4_0>(m, n_tiles, k, sink, s);
+    if (type == OPENMINI_QMM_Q8_0) return launch_ceiling<OPENMINI_QMM_Q8_0>(m, n_tiles, k, sink, s);
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
                             bool gate_in_y) {

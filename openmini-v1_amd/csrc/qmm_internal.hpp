@@ -188,6 +188,9 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
 // gate_in_y: y holds gate = x . Wg^T on entry; each element becomes silu(gate) * (x . W^T).
 hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s,
                             bool gate_in_y = false);
+// The GEMM's register-only instruction mix on its grid for an m x n x k Q4_0 / Q8_0
+// problem (compute-only ceiling); sink[0] is written only if a sentinel is hit.
+hipError_t launch_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, float* sink, hipStream_t s);
 
 // quant_simd::convert_to_soa_layout: output bytes, and the conversion of `len` device
 // bytes (n elements) into `out` on stream s.

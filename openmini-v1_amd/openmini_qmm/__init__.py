@@ -12,4 +12,5 @@ from .ops import (DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,
                   UnsupportedType, convert_to_soa_layout, dequantize, dequantize_simd,
                   get_gemm_engine, init, linear,
                   linear_gemm, safe_dequantize, safe_dequantize_q4_0, safe_dequantize_q4_1,
-                  safe_dequantize_q8_0, stream_copy, stream_read)
+                  safe_dequantize_q8_0, stream_copy, stream_read,
+                  gemm_ceiling)

@@ -120,6 +120,7 @@ SIGNATURES = {
     "openmini_qmm_stream_synchronize": (_i, [_p]),
     "openmini_qmm_stream_copy": (_i, [_p, _p, _sz, _p]),
     "openmini_qmm_stream_read": (_i, [_p, _sz, _p, _p]),
+    "openmini_qmm_gemm_ceiling": (_i, [_i, _i64, _i64, _i64, _p, _p]),
     "openmini_qmm_soa_bytes": (_i, [_i, _sz, _sz, ctypes.POINTER(_sz)]),
     "openmini_qmm_convert_to_soa_device": (_i, [_i, _p, _sz, _sz, _p, _p]),
     "openmini_qmm_convert_to_soa": (_i, [_i, _p, _sz, _sz, _p]),

@@ -154,6 +154,12 @@ def stream_read(src: DeviceBuffer, nbytes: int, sink: DeviceBuffer, stream=None)
     assert nbytes <= src.nbytes and sink.nbytes >= 4
     check(lib().openmini_qmm_stream_read(src.ptr, nbytes, sink.ptr, stream))
 
+def gemm_ceiling(qtype: int, m: int, n: int, k: int, sink: DeviceBuffer, stream=None) -> None:
+    """The prefill GEMM's compute-only ceiling (openmini_qmm_gemm_ceiling): its grid and
+    per-block register work for an m x n x k Q4_0 / Q8_0 problem, without memory
+    traffic.  `sink` (4 bytes) is written only if a sentinel is hit."""
+    check(lib().openmini_qmm_gemm_ceiling(int(qtype), int(m), int(n), int(k), sink.ptr, stream))
+
 
 def init(device: int = 0) -> None:
     check(lib().openmini_qmm_init(device))

@@ -136,6 +136,7 @@ extern "C" {
     pub fn openmini_qmm_stream_synchronize(stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_stream_copy(d_dst: *mut c_void, d_src: *const c_void, bytes: usize, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_stream_read(d_src: *const c_void, bytes: usize, d_sink: *mut c_void, stream: *mut c_void) -> c_int;
+    pub fn openmini_qmm_gemm_ceiling(tensor_type: c_int, m: i64, n: i64, k: i64, d_sink: *mut c_void, stream: *mut c_void) -> c_int;
 }
 
 /// Status -> Result with the calling thread's openmini_qmm_last_error() message.

@@ -82,6 +82,11 @@ def test_host_only_validation():
     assert b"null weight" in L.openmini_qmm_last_error()
     assert L.openmini_qmm_ffn_gate_up(None, None, p, p, 1, None) == _native.ERR_INVALID_PARAM
     assert L.openmini_qmm_ffn_gate_up_bf16(None, None, p, p, 1, None) == _native.ERR_INVALID_PARAM
+    # the GEMM ceiling yardstick validates before touching a device
+    assert L.openmini_qmm_gemm_ceiling(7, 512, 11008, 4096, None, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemm_ceiling(12, 512, 11008, 4096, p, None) == _native.ERR_UNSUPPORTED
+    assert L.openmini_qmm_gemm_ceiling(7, 512, 11008, 4100, p, None) == _native.ERR_INVALID_PARAM
+    assert L.openmini_qmm_gemm_ceiling(7, 0, 11008, 4096, p, None) == _native.ERR_INVALID_PARAM
 
 
 def test_python_mirror_raises_reference_errors():
