@@ -584,12 +584,14 @@ def main(argv=None) -> int:
             log(f"decode {shapes[-1]['workload']}: {r['kernel_ms'] * 1e3:.2f} us, {r['gbs_kernel']:.1f} GB/s")
     kquant = []
     if not args.no_shapes:
-        # decode GEMV on K-quant weights (Llama-7B up / down shapes, batch 1)
-        for qtype, n, k, seed in ((Q4_K, 11008, 4096, 0x5EED0071), (Q4_K, 4096, 11008, 0x5EED0072),
-                                  (Q6_K, 11008, 4096, 0x5EED0073), (Q6_K, 4096, 11008, 0x5EED0074)):
+        # decode GEMV on K-quant weights (Llama-7B up / down shapes at batch 1; the up
+        # shape at batch 8 through the batched kernel)
+        for qtype, n, k, b, seed in ((Q4_K, 11008, 4096, 1, 0x5EED0071), (Q4_K, 4096, 11008, 1, 0x5EED0072),
+                                     (Q6_K, 11008, 4096, 1, 0x5EED0073), (Q6_K, 4096, 11008, 1, 0x5EED0074),
+                                     (Q4_K, 11008, 4096, 8, 0x5EED0075), (Q6_K, 11008, 4096, 8, 0x5EED0076)):
             r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
-                           qtype=qtype, batch=1, seed=seed)
-            kquant.append({"workload": f"{TYPE_NAME[qtype]}_gemv_n{n}_k{k}_b1", "unit": "GB/s",
+                           qtype=qtype, batch=b, seed=seed)
+            kquant.append({"workload": f"{TYPE_NAME[qtype]}_gemv_n{n}_k{k}_b{b}", "unit": "GB/s",
                            "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                            "frac": round(r["gbs_kernel"] / HBM_PEAK_GBS, 4),
                            "alg_bytes_per_step": r["alg_bytes_per_step"], "sha256": r["sha256"]})

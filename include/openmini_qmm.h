@@ -156,8 +156,7 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
 /* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
  * Any batch >= 1.  Up to 4 rows: the single-row-tuned kernel (one launch per 4
  * rows); 5 or more: the batched kernel, one pass over W per 16 rows, in which a
- * row's result does not depend on the other rows of the call (Q4_K / Q6_K weights
- * use the single-row kernel for every batch, one launch per 4 rows).
+ * row's result does not depend on the other rows of the call.  Every weight type.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);

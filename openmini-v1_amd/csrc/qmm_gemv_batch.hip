@@ -6,9 +6,13 @@
 // sgemm over weights dequantized at load.
 //
 // Arithmetic (every product exact, fp32 accumulation):
-//   * Codes are exact in fp16: Q4_0 as q - 8, Q8_0 as q.  They are built from the
-//     code bytes with the 1024 + u pattern (0x64XX is the fp16 1024 + XX, spacing 1)
-//     and one packed fp16 subtraction.
+//   * Codes are exact in fp16: Q4_0 / Q4_K as q - 8, Q8_0 as q, Q6_K as q in
+//     [-32, 31].  They are built from the code bytes with the 1024 + u pattern
+//     (0x64XX is the fp16 1024 + XX, spacing 1) and one packed fp16 subtraction.
+//   * K-quant weights (the reference's reading, quant.rs:338-410 and :515-600) use
+//     their 32-element sub-blocks as the blocks, with block factor d * scale (exact).
+//     Q6_K's scale changes every 16 elements, inside one MFMA's 32: each half runs its
+//     own MFMA pair with the other half's codes zeroed, scaled by its own factor.
 //   * Per (batch row, 4-block group) the activations are scaled by 2^s, s chosen so
 //     the group's largest |x| lands in [2^14, 2^15), and split exactly into
 //     hi = x' with its low 13 mantissa bits cleared (11 significant bits, an fp16
@@ -137,24 +141,53 @@ __device__ __forceinline__ void broadcast4(float v, float* out) {
 // One group's operands in registers: the lane's activations of the 4 blocks and, per
 // (weight, tile) pair, chunk slot `lane` (block lane / 16, row lane % 16) -- its codes
 // and scale, one wide load each -- later transposed to the MFMA lanes.
-template <bool kQ4, int kNT>
+// Chunk geometry by weight format (layouts in qmm_internal.hpp).
+template <int kFmt>
+struct BFmt {
+    static constexpr bool kQ8 = kFmt == OPENMINI_QMM_Q8_0;
+    static constexpr bool kQ4K = kFmt == OPENMINI_QMM_Q4_K;
+    static constexpr bool kQ6K = kFmt == OPENMINI_QMM_Q6_K;
+    static constexpr bool kKQ = kQ4K || kQ6K;
+    static constexpr bool kNib = !kQ8 && !kQ6K;  // Q4_0 / Q4_K: the codes are nibbles q ^ 8
+    static constexpr int kCB = kQ8 ? 32 : 16;      // bytes of a slot's (low) codes
+    static constexpr int kScaleOff = kTileEntries * (kQ6K ? 24 : kCB);
+    static constexpr int kDOff = kScaleOff + (kQ6K ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
+    static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ6K ? kQ6KChunk : chunk_bytes_for(!kQ8);
+};
+
+template <int kFmt, int kNT>
 struct Stage {
     float x[4][8];
-    uint4 c[kNT][kQ4 ? 1 : 2];
+    uint4 c[kNT][BFmt<kFmt>::kQ8 ? 2 : 1];
+    uint2 hb[BFmt<kFmt>::kQ6K ? kNT : 1];  // Q6_K: the slot's top code bits
     uint32_t sc[kNT];
+    uint32_t dk[BFmt<kFmt>::kKQ ? kNT : 1];  // K-quant: the fp16 d of the slot's row
 };
+
+// Q6_K low-nibble word kq and top-bit word kq / 2 of a slot -> 8 fp16 q, elements
+// 8 kq .. 8 kq + 7 in order: bytes u = (q & 63) ^ 32 = q + 32 through the 1024 + u
+// pattern, minus 1056.
+__device__ __forceinline__ f16x8 codes_q6(uint32_t w, uint32_t hm, int kq) {
+    const int f = (kq & 1) * 4;  // bit of field 2 (kq & 1); field + 1 for elements + 4..7
+    const uint32_t lo = ((w & 0x0F0F0F0Fu) | (((hm >> f) & 0x03030303u) << 4)) ^ 0x20202020u;
+    const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) | (((hm >> (f + 2)) & 0x03030303u) << 4)) ^ 0x20202020u;
+    uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1056.0f),
+                     pk_sub(magic_pair(hi, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1056.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
 
 // Workgroup: T row tiles of kNW weights, W waves splitting K.  A wave walks its slice
 // one group at a time with the next group's loads in flight (two register stages).
-template <bool kQ4, int T, int W, int kNW>
+template <int kFmt, int T, int W, int kNW>
 __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __restrict__ w0,
                                                             const uint8_t* __restrict__ w1,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int n_rows, int n_tiles, int groups, int k, int batch) {
     constexpr int kNT = kNW * T;  // (weight, tile) pairs of the workgroup
-    constexpr int kCB = kQ4 ? 16 : 32;
+    using F = BFmt<kFmt>;
+    constexpr int kCB = F::kCB;
     constexpr int kCodeBytes = kTileEntries * kCB;
-    constexpr int kChunk = chunk_bytes_for(kQ4);
+    constexpr int kChunk = F::kChunk;
     // per wave: the 16 A rows' 2^-s of the current group while running, then the
     // partial sums [W][kNT][64 lanes][4] for the reduction
     constexpr int kRed = W * kNT * 256;
@@ -185,7 +218,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     for (int i = 0; i < kNT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Issue group g's loads: activations first (L2 hits), then the chunks.
-    auto load = [&](Stage<kQ4, kNT>& st, int g) {
+    auto load = [&](Stage<kFmt, kNT>& st, int g) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t e = (uint32_t)g * 128u + t * 32u + kq * 8u;
@@ -200,16 +233,24 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             const __amdgpu_buffer_rsrc_t rs = i / T == 0 ? w_rs0 : w_rs1;
             const uint32_t soff = tile_off[i % T] + (uint32_t)g * kChunk;
             st.c[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * kCB, soff, 0));
-            if constexpr (!kQ4)
+            if constexpr (F::kQ8)
                 st.c[i][1] =
                     __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * kCB + 16, soff, 0));
-            st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, kCodeBytes + lane * 2, soff, 0);
+            if constexpr (F::kQ6K)
+                st.hb[i] = __builtin_bit_cast(
+                    uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, kCodeBytes + lane * 8, soff, 0));
+            if constexpr (F::kQ4K)
+                st.sc[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, F::kScaleOff + lane, soff, 0);
+            else
+                st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, F::kScaleOff + lane * 2, soff, 0);
+            if constexpr (F::kKQ)  // the d of slot lane's row, lane % 16
+                st.dk[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, F::kDOff + li * 2, soff, 0);
         }
     };
 
     // One group: the range scale and hi / lo split of the activations (shared by the
     // kNT pairs), then per pair 4 blocks of 2 MFMAs and the scale FMAs.
-    auto compute = [&](const Stage<kQ4, kNT>& st) {
+    auto compute = [&](const Stage<kFmt, kNT>& st) {
         float m = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -232,29 +273,61 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             // lane (kq, i) takes word kq (Q4_0) / words 2 kq, 2 kq + 1 (Q8_0) of slot
             // (t, i) for t = 0..3, and the scales of its column
             uint32_t e[4], o[4];
-            if constexpr (kQ4) {
+            if constexpr (!F::kQ8) {
                 e[0] = st.c[i][0].x; e[1] = st.c[i][0].y; e[2] = st.c[i][0].z; e[3] = st.c[i][0].w;
                 transpose4(e[0], e[1], e[2], e[3]);
+                if constexpr (F::kQ6K) {
+                    // lane (kq, i) takes top-bit word kq / 2 of slot (t, i): the loader
+                    // lane's registers are words 0, 0, 1, 1 before the transpose
+                    o[0] = st.hb[i].x; o[1] = st.hb[i].x; o[2] = st.hb[i].y; o[3] = st.hb[i].y;
+                    transpose4(o[0], o[1], o[2], o[3]);
+                }
             } else {
                 e[0] = st.c[i][0].x; o[0] = st.c[i][0].y; e[1] = st.c[i][0].z; o[1] = st.c[i][0].w;
                 e[2] = st.c[i][1].x; o[2] = st.c[i][1].y; e[3] = st.c[i][1].z; o[3] = st.c[i][1].w;
                 transpose4(e[0], e[1], e[2], e[3]);
                 transpose4(o[0], o[1], o[2], o[3]);
             }
-            float ds[4];
-            broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
+            // the block factors of column i (slot (t, i) for t = 0..3), exact in fp32:
+            // the fp16 scale; Q4_K d * scale; Q6_K d * scale of each 16-element half
+            float ds[4], ds1[4];
+            if constexpr (F::kQ4K) {
+                broadcast4(f16_bits_to_f32((uint16_t)st.dk[i]) * (float)(st.sc[i] & 0xFFu), ds);
+            } else if constexpr (F::kQ6K) {
+                const float dd = f16_bits_to_f32((uint16_t)st.dk[i]);
+                broadcast4(dd * (float)(int8_t)(st.sc[i] & 0xFFu), ds);
+                broadcast4(dd * (float)(int8_t)((st.sc[i] >> 8) & 0xFFu), ds1);
+            } else {
+                broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
+            }
             f32x4 gs = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 f16x8 b;
-                if constexpr (kQ4)
+                if constexpr (F::kNib)
                     b = codes_q4(e[t]);
+                else if constexpr (F::kQ6K)
+                    b = codes_q6(e[t], o[t], kq);
                 else
                     b = codes_q8(e[t], o[t]);
-                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
+                if constexpr (F::kQ6K) {
+                    // the halves carry their own factors: lanes kq = 0, 1 hold the
+                    // block's elements 0..15, lanes 2, 3 elements 16..31; one MFMA pair
+                    // per half with the other half's codes zeroed
+                    const f16x8 z = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                    const f16x8 b0 = kq < 2 ? b : z, b1 = kq < 2 ? z : b;
+                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b0, d0, 0, 0, 0);
+                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b1, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b1, d1, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds[t], gs[r]);
+                    for (int r = 0; r < 4; ++r) gs[r] = fmaf(d1[r], ds1[t], fmaf(d0[r], ds[t], gs[r]));
+                } else {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds[t], gs[r]);
+                }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(gs[r], rs[r], acc[i][r]);
@@ -263,7 +336,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     };
 
     if (g0 < g1) {  // uniform per wave
-        Stage<kQ4, kNT> sa, sb;
+        Stage<kFmt, kNT> sa, sb;
         int g = g0;
         load(sa, g);
         // the loads past the slice end re-read its last group (cache hits) and are
@@ -306,19 +379,18 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     }
 }
 
-template <bool kQ4, int T, int W, int kNW>
+template <int kFmt, int T, int W, int kNW>
 hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch, hipStream_t s) {
     const unsigned wgs = (unsigned)((w.n_tiles + T - 1) / T);
-    hipLaunchKernelGGL((gemv_batch_kernel<kQ4, T, W, kNW>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x, y,
+    hipLaunchKernelGGL((gemv_batch_kernel<kFmt, T, W, kNW>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x, y,
                        (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch);
     return hipGetLastError();
 }
 
 }  // namespace
 
-// Q4_K / Q6_K weights run the single-row kernel at every batch (one launch per 4 rows).
 bool use_batch_kernel(const Weight& w, int64_t batch) {
-    return batch >= kBatchMin && !is_kquant(w.type) && (int64_t)kBatchRows * w.k * 4 <= INT32_MAX;
+    return batch >= kBatchMin && (int64_t)kBatchRows * w.k * 4 <= INT32_MAX;
 }
 
 hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, float* y, int64_t batch,
@@ -344,23 +416,24 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 
 // Launch shape, measured on MI355X (Q4_0 / Q8_0, B = 4, 8, 16, N = 4096 ... 28672):
 // four waves per workgroup; tiles per workgroup so that the grid stays near one
-// workgroup per CU (256 row tiles -> 1, 512 -> 2, 1024 -> 4, more -> 8; Q8_0 at most
-// 4, whose 8-tile registers would leave one wave per SIMD).  More tiles share each
-// wave's activation loads and split; more workgroups than CUs add activation re-reads.
+// workgroup per CU (256 row tiles -> 1, 512 -> 2, 1024 -> 4, more -> 8; Q8_0 and Q6_K
+// at most 4, whose 8-tile registers would leave one wave per SIMD).  More tiles share
+// each wave's activation loads and split; more workgroups than CUs add activation
+// re-reads.
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     (void)batch;
     BatchShape sh{};
-    const bool q4 = w.type == OPENMINI_QMM_Q4_0;
+    const bool q4 = w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K;
     sh.t = pair || w.n_tiles <= 256 ? 1 : w.n_tiles <= 512 ? 2 : (w.n_tiles <= 1024 || !q4) ? 4 : 8;
     sh.w = w.groups >= 8 ? 4 : 1;
     return sh;
 }
 
-template <bool kQ4, int kNW>
+template <int kFmt, int kNW>
 static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
                                  const BatchShape& sh, hipStream_t s) {
 #define QMM_BATCH_CASE(T_, W_)                                                            \
-    if (sh.t == T_ && sh.w == W_) return run<kQ4, T_, W_, kNW>(w, w1, x, y, batch, s);
+    if (sh.t == T_ && sh.w == W_) return run<kFmt, T_, W_, kNW>(w, w1, x, y, batch, s);
     // 1024-thread workgroups leave 128 registers a wave: one tile of one weight only
     QMM_BATCH_CASE(1, 1)
     QMM_BATCH_CASE(1, 4)
@@ -372,7 +445,7 @@ static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float
         QMM_BATCH_CASE(2, 8)
         QMM_BATCH_CASE(4, 4)
         QMM_BATCH_CASE(4, 8)
-        if constexpr (kQ4) {
+        if constexpr (BFmt<kFmt>::kNib) {
             QMM_BATCH_CASE(8, 4)
         }
     }
@@ -384,12 +457,22 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
                              const BatchShape& sh, hipStream_t s) {
     if (batch < 1 || batch > kBatchRows) return hipErrorInvalidValue;
     if ((int64_t)batch * w.k * 4 > INT32_MAX) return hipErrorInvalidValue;  // 31-bit x offsets
-    const bool q4 = w.type == OPENMINI_QMM_Q4_0;
-    if (up)
-        return q4 ? dispatch_batch<true, 2>(w, up->chunks, x, y, batch, sh, s)
-                  : dispatch_batch<false, 2>(w, up->chunks, x, y, batch, sh, s);
-    return q4 ? dispatch_batch<true, 1>(w, nullptr, x, y, batch, sh, s)
-              : dispatch_batch<false, 1>(w, nullptr, x, y, batch, sh, s);
+    const uint8_t* w1 = up ? up->chunks : nullptr;
+    switch (w.type) {
+    case OPENMINI_QMM_Q4_0:
+        return up ? dispatch_batch<OPENMINI_QMM_Q4_0, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_batch<OPENMINI_QMM_Q4_0, 1>(w, w1, x, y, batch, sh, s);
+    case OPENMINI_QMM_Q8_0:
+        return up ? dispatch_batch<OPENMINI_QMM_Q8_0, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_batch<OPENMINI_QMM_Q8_0, 1>(w, w1, x, y, batch, sh, s);
+    case OPENMINI_QMM_Q4_K:
+        return up ? dispatch_batch<OPENMINI_QMM_Q4_K, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_batch<OPENMINI_QMM_Q4_K, 1>(w, w1, x, y, batch, sh, s);
+    case OPENMINI_QMM_Q6_K:
+        return up ? dispatch_batch<OPENMINI_QMM_Q6_K, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_batch<OPENMINI_QMM_Q6_K, 1>(w, w1, x, y, batch, sh, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace qmm

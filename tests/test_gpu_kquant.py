@@ -69,6 +69,10 @@ def test_kquant_one_hot_columns_exact(qmm, orc, qtype):
     y = np.concatenate([gemv_nan_filled(qmm, w, x[i:i + 4]) for i in range(0, len(cols), 4)])
     for i, c in enumerate(cols):
         assert np.array_equal(y[i], W[:, c]), (c, np.nonzero(y[i] != W[:, c]))
+    # all ten rows in one call: the batched kernel (fp16 codes and hi / lo activations)
+    yb = gemv_nan_filled(qmm, w, x)
+    for i, c in enumerate(cols):
+        assert np.array_equal(yb[i], W[:, c]), (c, np.nonzero(yb[i] != W[:, c]))
 
 
 def test_q4_k_nonfinite_dmin_poisons_its_rows(qmm, orc):
@@ -149,6 +153,54 @@ def test_kquant_upload_from_device_any_alignment(qmm, orc, qtype, offset):
     y = gemv_nan_filled(qmm, w_dev, x)
     assert np.array_equal(y.view(np.uint32), gemv_nan_filled(qmm, w_host, x).view(np.uint32))
     assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x), TOL, f"offset {offset}")
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("N,K", [(1, 256), (37, 512), (130, 2304), (1000, 4096)])
+@pytest.mark.parametrize("B", [5, 8, 16, 21])
+def test_kquant_batch_parity(qmm, orc, qtype, N, K, B):
+    """Five and more rows go through the batched kernel (one pass over W for up to 16
+    rows): ragged tiles, an odd super-block count, a batch split into 16 + 5."""
+    print(f"kquant gemv batch type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xCD00 + N + K + B)
+    x = synth.normal(0xCD01 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    assert_parity(gemv_nan_filled(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} K={K} B={B}")
+
+
+@pytest.mark.parametrize("qtype,N,K,B", [(Q4_K, 11008, 4096, 8), (Q6_K, 11008, 4096, 8),
+                                         (Q4_K, 4096, 11008, 16), (Q6_K, 4096, 11008, 16)])
+def test_kquant_batch_llama_shapes(qmm, orc, qtype, N, K, B):
+    print(f"kquant gemv batch type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xCE00 + N + B)
+    x = synth.normal(0xCE01 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    print(assert_parity(gemv_nan_filled(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, "llama"))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_batch_rows_independent(qmm, qtype):
+    """A row's output in the batched kernel depends only on its own activations: the
+    first 8 rows of a 16-row call equal an 8-row call bit for bit."""
+    N, K = 640, 2048
+    blocks = synth.kquant_blocks(qtype, N, K, seed=0xCF00 + qtype)
+    x = synth.normal(0xCF01, (16, K), 1.0)
+    x[8:] *= 1e3
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    y16, y8 = gemv_nan_filled(qmm, w, x), gemv_nan_filled(qmm, w, x[:8])
+    assert np.array_equal(y16[:8].view(np.uint32), y8.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_kquant_batch_ffn_gate_up(qmm, orc, qtype):
+    """silu(x . Wg^T) * (x . Wu^T) for 8 rows through the batched kernel's pair kind."""
+    N, K, B = 1280, 1024, 8
+    bg, bu = synth.kquant_blocks(qtype, N, K, 0xD000), synth.kquant_blocks(qtype, N, K, 0xD001)
+    wg, wu = qmm.QuantizedWeight(qtype, bg, N, K), qmm.QuantizedWeight(qtype, bu, N, K)
+    x = synth.normal(0xD002, (B, K), 1.0)
+    dx, dh = qmm.DeviceBuffer.from_numpy(x), qmm.DeviceBuffer(B * N * 4)
+    qmm.ffn_gate_up(wg, wu, dx, dh, B)
+    assert_parity(dh.download(np.float32, (B, N)), orc.ffn_hidden_f64(qtype, bg, bu, N, K, x), TOL, "hidden")
 
 
 def test_kquant_error_paths(qmm):
