@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
     const int64_t row0 = rt * kTileRows, s0 = 2 * q;
     const uint32_t delta = (uint32_t)((uintptr_t)gguf & 3u);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(gguf - delta), (short)0, (int)(src_bytes + delta), 0x00020000);
+        reinterpret_cast<void*>((uintptr_t)gguf & ~(uintptr_t)3), (short)0, (int)(src_bytes + delta), 0x00020000);
     // byte offset of row r's span from the aligned base (fits: src_bytes + 3 < 2^32)
     auto span_off = [&](int r) {
         return (uint32_t)(((row0 + r) * supers + s0) * kBPB) + delta;
