@@ -92,6 +92,19 @@ def test_q4_k_nonfinite_dmin_poisons_its_rows(qmm, orc):
     assert not np.any(np.isfinite(ref[:, bad])) and not np.any(np.isfinite(y[:, bad]))
     good = [n for n in range(N) if n not in bad]
     assert_parity(y[:, good], ref[:, good], TOL, "finite rows")
+    # the batched kernel (8 rows) and the prefill GEMM poison exactly the same rows
+    x8 = synth.normal(0xC302, (8, K), 1.0)
+    y8 = gemv_nan_filled(qmm, w, x8)
+    with np.errstate(invalid="ignore"):
+        ref8 = orc.linear_f64(Q4_K, blocks, N, K, x8)
+    assert not np.any(np.isfinite(y8[:, bad]))
+    assert_parity(y8[:, good], ref8[:, good], TOL, "finite rows, batched")
+    xb = synth.to_bf16_bits(synth.normal(0xC303, (130, K), 1.0))
+    ym = run_gemm(qmm, w, xb)
+    with np.errstate(invalid="ignore"):
+        refm = orc.linear_bf16x_f64(Q4_K, blocks, N, K, xb)
+    assert not np.any(np.isfinite(ym[:, bad]))
+    assert_parity(ym[:, good], refm[:, good], TOL, "finite rows, gemm")
 
 
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
