@@ -414,17 +414,22 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
     return hipSuccess;
 }
 
-// Launch shape, measured on MI355X (Q4_0 / Q8_0, B = 4, 8, 16, N = 4096 ... 28672):
-// four waves per workgroup; tiles per workgroup so that the grid stays near one
-// workgroup per CU (256 row tiles -> 1, 512 -> 2, 1024 -> 4, more -> 8; Q8_0 and Q6_K
-// at most 4, whose 8-tile registers would leave one wave per SIMD).  More tiles share
-// each wave's activation loads and split; more workgroups than CUs add activation
-// re-reads.
+// Launch shape, measured on MI355X (Q4_0 / Q8_0 / Q4_K, B = 8, 16, N = 4096 ... 28672):
+// four waves per workgroup (one when K has fewer than 8 groups); tiles per workgroup
+// so that the grid is one workgroup per CU, all CUs busy: T = ceil(tiles / 256), at
+// most 8 (Q4_0 / Q4_K) or 4 (Q8_0 / Q6_K, whose 8-tile registers would leave one
+// wave per SIMD).  More tiles share each wave's activation loads and split; more
+// workgroups than CUs add activation re-reads.  Against powers of two (1, 2, 4, 8):
+// 11008 x 4096 (688 tiles) T = 3 vs 4: Q8_0 B = 8 13.7-15.1 vs 15.8-16.8 us, Q4_0
+// B = 16 13.1 vs 15.2 us, Q4_K B = 8 13.0 vs 14.8 us; 28672 x 8192 (1792 tiles) T = 7
+// vs 8: 45.4 vs 47.8 us.  A (gate, up) pair runs one tile per workgroup.
+constexpr int64_t kCUs = 256;  // MI355X compute units
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     (void)batch;
     BatchShape sh{};
-    const bool q4 = w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K;
-    sh.t = pair || w.n_tiles <= 256 ? 1 : w.n_tiles <= 512 ? 2 : (w.n_tiles <= 1024 || !q4) ? 4 : 8;
+    const int64_t cap = (w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K) ? 8 : 4;
+    const int64_t per_cu = (w.n_tiles + kCUs - 1) / kCUs;
+    sh.t = pair ? 1 : (int)(per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu);
     sh.w = w.groups >= 8 ? 4 : 1;
     return sh;
 }
@@ -432,21 +437,20 @@ BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
 template <int kFmt, int kNW>
 static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
                                  const BatchShape& sh, hipStream_t s) {
-#define QMM_BATCH_CASE(T_, W_)                                                            \
-    if (sh.t == T_ && sh.w == W_) return run<kFmt, T_, W_, kNW>(w, w1, x, y, batch, s);
-    // 1024-thread workgroups leave 128 registers a wave: one tile of one weight only
-    QMM_BATCH_CASE(1, 1)
-    QMM_BATCH_CASE(1, 4)
-    QMM_BATCH_CASE(1, 8)
+#define QMM_BATCH_CASE(T_)                                                                     \
+    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW>(w, w1, x, y, batch, s)          \
+                                     : run<kFmt, T_, 1, kNW>(w, w1, x, y, batch, s);
+    if (sh.w != 1 && sh.w != 4) return hipErrorInvalidValue;
+    QMM_BATCH_CASE(1)
     if constexpr (kNW == 1) {
-        QMM_BATCH_CASE(1, 16)
-        QMM_BATCH_CASE(2, 1)
-        QMM_BATCH_CASE(2, 4)
-        QMM_BATCH_CASE(2, 8)
-        QMM_BATCH_CASE(4, 4)
-        QMM_BATCH_CASE(4, 8)
+        QMM_BATCH_CASE(2)
+        QMM_BATCH_CASE(3)
+        QMM_BATCH_CASE(4)
         if constexpr (BFmt<kFmt>::kNib) {
-            QMM_BATCH_CASE(8, 4)
+            QMM_BATCH_CASE(5)
+            QMM_BATCH_CASE(6)
+            QMM_BATCH_CASE(7)
+            QMM_BATCH_CASE(8)
         }
     }
 #undef QMM_BATCH_CASE

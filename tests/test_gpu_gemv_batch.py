@@ -45,6 +45,32 @@ def test_batch_baseline_shapes(qmm, orc, qtype, N, K, B):
     print(assert_parity(run_gemv(qmm, w, x), orc.linear_f64(qtype, blocks, N, K, x), TOL, "baseline"))
 
 
+@pytest.mark.parametrize("qtype,N,K,B", [
+    (Q4_0, 16 * 700, 1024, 8),     # 700 row tiles: 3 per workgroup
+    (Q4_0, 16 * 1100, 512, 16),    # 5 per workgroup, one wave (K < 8 groups)
+    (Q4_0, 16 * 1400, 1024, 6),    # 6
+    (Q4_0, 16 * 1700, 1024, 16),   # 7
+    (Q4_0, 16 * 2000 + 5, 1024, 9),  # 8, ragged last tile
+    (Q8_0, 16 * 700 + 3, 1024, 8),   # 3 (Q8_0 stops at 4)
+    (Q8_0, 16 * 1500, 1024, 16),   # 4
+    (12, 16 * 1100, 1024, 8),      # Q4_K, 5
+    (14, 16 * 700, 1024, 8),       # Q6_K, 3
+])
+def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
+    """Every tiles-per-workgroup count the launch rule picks (ceil(tiles / 256), at
+    most 8 or 4) against the oracle on all N outputs; y is NaN-filled first, so a
+    tile the kernel skips fails."""
+    print(f"gemv batch tiles type={qtype} N={N} K={K} B={B}", flush=True)
+    blocks = (synth.kquant_blocks(qtype, N, K, seed=0xB500 + N) if qtype in (12, 14)
+              else synth.weight_blocks(qtype, N, K, seed=0xB500 + N))
+    x = synth.normal(0xB501 + B, (B, K), 1.0)
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+    dx, dy = qmm.DeviceBuffer.from_numpy(x), qmm.DeviceBuffer(B * N * 4)
+    dy.fill(0xFF)
+    w.gemv(dx, dy, B)
+    assert_parity(dy.download(np.float32, (B, N)), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} B={B}")
+
+
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_batch_rows_independent(qmm, qtype):
     """A row's result does not depend on the other rows of the batch (each MFMA row
