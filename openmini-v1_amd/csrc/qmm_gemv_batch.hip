@@ -422,14 +422,18 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 // workgroups than CUs add activation re-reads.  Against powers of two (1, 2, 4, 8):
 // 11008 x 4096 (688 tiles) T = 3 vs 4: Q8_0 B = 8 13.7-15.1 vs 15.8-16.8 us, Q4_0
 // B = 16 13.1 vs 15.2 us, Q4_K B = 8 13.0 vs 14.8 us; 28672 x 8192 (1792 tiles) T = 7
-// vs 8: 45.4 vs 47.8 us.  A (gate, up) pair runs one tile per workgroup.
+// vs 8: 45.4 vs 47.8 us.  A (gate, up) pair takes at most 4 (Q4_0 / Q4_K) or 3 tiles:
+// against one tile per workgroup, 11008 x 4096 Q4_0 B = 8 25.5 -> 20.8 us, Q8_0 B = 8
+// 30.7 -> 25.2 us, Q4_K B = 16 31.9 -> 22.5 us, 28672 x 8192 Q4_0 B = 16 118 -> 80 us.
 constexpr int64_t kCUs = 256;  // MI355X compute units
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     (void)batch;
     BatchShape sh{};
-    const int64_t cap = (w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K) ? 8 : 4;
+    // a pair holds two weights' registers per tile: at most 4 / 3 tiles
+    const bool nib = w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K;
+    const int64_t cap = pair ? (nib ? 4 : 3) : nib ? 8 : 4;
     const int64_t per_cu = (w.n_tiles + kCUs - 1) / kCUs;
-    sh.t = pair ? 1 : (int)(per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu);
+    sh.t = (int)(per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu);
     sh.w = w.groups >= 8 ? 4 : 1;
     return sh;
 }
@@ -442,8 +446,14 @@ static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float
                                      : run<kFmt, T_, 1, kNW>(w, w1, x, y, batch, s);
     if (sh.w != 1 && sh.w != 4) return hipErrorInvalidValue;
     QMM_BATCH_CASE(1)
+    QMM_BATCH_CASE(2)
+    if constexpr (kNW == 2) {
+        QMM_BATCH_CASE(3)
+        if constexpr (BFmt<kFmt>::kNib) {
+            QMM_BATCH_CASE(4)
+        }
+    }
     if constexpr (kNW == 1) {
-        QMM_BATCH_CASE(2)
         QMM_BATCH_CASE(3)
         QMM_BATCH_CASE(4)
         if constexpr (BFmt<kFmt>::kNib) {

@@ -148,6 +148,28 @@ def test_batch_ffn_gate_up(qmm, orc, qtype, N, K, B):
     np.testing.assert_allclose(h, orc.silu_f64(g) * u, rtol=1e-5, atol=1e-6 * float(np.max(np.abs(h))))
 
 
+@pytest.mark.parametrize("qtype,N,K,B", [
+    (Q4_0, 16 * 1100, 1024, 16),     # 4 tiles per workgroup (the pair cap)
+    (Q4_0, 16 * 600 + 7, 512, 8),    # 3, one wave, ragged last tile
+    (Q8_0, 16 * 700, 1024, 8),       # 3 (the pair cap for Q8_0 / Q6_K)
+    (12, 16 * 600, 1024, 8),         # Q4_K, 3
+    (14, 16 * 700 + 5, 1024, 6),     # Q6_K, 3, ragged
+])
+def test_batch_ffn_gate_up_tiles(qmm, orc, qtype, N, K, B):
+    """The pair kernel with several row tiles per workgroup, on all N outputs of a
+    NaN-filled h."""
+    print(f"ffn_gate_up batch tiles type={qtype} N={N} K={K} B={B}", flush=True)
+    make = (lambda sd: synth.kquant_blocks(qtype, N, K, sd)) if qtype in (12, 14) else \
+        (lambda sd: synth.weight_blocks(qtype, N, K, seed=sd))
+    bg, bu = make(0xB600 + N), make(0xB601 + N)
+    wg, wu = qmm.QuantizedWeight(qtype, bg, N, K), qmm.QuantizedWeight(qtype, bu, N, K)
+    x = synth.normal(0xB602 + B, (B, K), 1.0)
+    dx, dh = qmm.DeviceBuffer.from_numpy(x), qmm.DeviceBuffer(B * N * 4)
+    dh.fill(0xFF)
+    qmm.ffn_gate_up(wg, wu, dx, dh, B)
+    assert_parity(dh.download(np.float32, (B, N)), orc.ffn_hidden_f64(qtype, bg, bu, N, K, x), TOL, "hidden")
+
+
 def test_batch_gemv_multi(qmm, orc):
     """gemv_multi with a batch runs one batched pass per weight."""
     shapes = ((4096, 4096), (1024, 4096), (1024, 4096))
