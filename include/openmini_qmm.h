@@ -154,9 +154,10 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
  * gemm_engine.rs:40), on the quantized W without materialising f32 weights. */
 
 /* Decode GEMV: y[batch, N] = x[batch, K] . W^T, fp32 activations, fp32 output.
- * Any batch >= 1.  Up to 4 rows: the single-row-tuned kernel (one launch per 4
- * rows); 5 or more: the batched kernel, one pass over W per 16 rows, in which a
- * row's result does not depend on the other rows of the call.  Every weight type.
+ * Any batch >= 1.  Up to 3 rows: the single-row-tuned kernel; 4 or more: the
+ * batched kernel, one pass over W per 16 rows, in which a row's result does not
+ * depend on the other rows of the call nor on the batch size (bitwise).  Every
+ * weight type.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);

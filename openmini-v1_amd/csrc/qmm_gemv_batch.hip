@@ -85,16 +85,28 @@ __device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
 }
 
-// 8 scaled activations -> fp16 hi and lo parts (hi + lo = x' up to lo's rounding).
+// x - hi for the fp16 hi in the low (kHalf = 0) or high half of h, exact in fp32: one
+// mixed-precision FMA reading hi's half directly.
+template <int kHalf>
+__device__ __forceinline__ float minus_half(uint32_t h, float x) {
+    float r;
+    if constexpr (kHalf == 0)
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+
+// 8 scaled activations -> fp16 hi and lo parts: hi = x' rounded toward zero to fp16
+// (11 significant bits for x' >= 2^-14), lo = x' - hi, exact in fp32, rounded toward
+// zero to fp16.
 __device__ __forceinline__ void split8(const float* v, int s, f16x8& hi, f16x8& lo) {
     uint32_t h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const float a = __builtin_amdgcn_ldexpf(v[2 * j], s), b = __builtin_amdgcn_ldexpf(v[2 * j + 1], s);
-        const float ah = __uint_as_float(__float_as_uint(a) & 0xFFFFE000u);
-        const float bh = __uint_as_float(__float_as_uint(b) & 0xFFFFE000u);
-        h[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ah, bh));
-        l[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - ah, b - bh));
+        h[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+        l[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(minus_half<0>(h[j], a), minus_half<1>(h[j], b)));
     }
     hi = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(h));
     lo = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(l));
@@ -138,6 +150,25 @@ __device__ __forceinline__ void broadcast4(float v, float* out) {
     out[3] = __uint_as_float(b[1]);
 }
 
+// v from the lane kRot places further round its 16-lane row (DPP row_ror).
+template <int kRot>
+__device__ __forceinline__ float row_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + kRot, 0xF, 0xF, false));
+}
+
+// 8 fp16 values from lane li + kD (mod 16) of the lane's 16-lane row.
+template <int kD>
+__device__ __forceinline__ f16x8 from_lane(f16x8 v) {
+    // row_ror:n gives lane i the value of lane i - n
+    const uint4 u = __builtin_bit_cast(uint4, v);
+    constexpr int kCtl = 0x120 + (16 - kD);
+    return __builtin_bit_cast(
+        f16x8, uint4{(uint32_t)__builtin_amdgcn_mov_dpp((int)u.x, kCtl, 0xF, 0xF, false),
+                     (uint32_t)__builtin_amdgcn_mov_dpp((int)u.y, kCtl, 0xF, 0xF, false),
+                     (uint32_t)__builtin_amdgcn_mov_dpp((int)u.z, kCtl, 0xF, 0xF, false),
+                     (uint32_t)__builtin_amdgcn_mov_dpp((int)u.w, kCtl, 0xF, 0xF, false)});
+}
+
 // One group's operands in registers: the lane's activations of the 4 blocks and, per
 // (weight, tile) pair, chunk slot `lane` (block lane / 16, row lane % 16) -- its codes
 // and scale, one wide load each -- later transposed to the MFMA lanes.
@@ -155,9 +186,9 @@ struct BFmt {
     static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ6K ? kQ6KChunk : chunk_bytes_for(!kQ8);
 };
 
-template <int kFmt, int kNT>
+template <int kFmt, int kNT, int kXB>
 struct Stage {
-    float x[4][8];
+    float x[kXB][8];
     uint4 c[kNT][BFmt<kFmt>::kQ8 ? 2 : 1];
     uint2 hb[BFmt<kFmt>::kQ6K ? kNT : 1];  // Q6_K: the slot's top code bits
     uint32_t sc[kNT];
@@ -178,13 +209,24 @@ __device__ __forceinline__ f16x8 codes_q6(uint32_t w, uint32_t hm, int kq) {
 
 // Workgroup: T row tiles of kNW weights, W waves splitting K.  A wave walks its slice
 // one group at a time with the next group's loads in flight (two register stages).
-template <int kFmt, int T, int W, int kNW>
+// kRep lanes share each activation row (batches of at most 16 / kRep rows): lane
+// (kq, i) loads and splits blocks kXB p .. kXB p + kXB - 1 of batch row i % (16 / kRep),
+// p = i / (16 / kRep), so the group's split costs 1 / kRep of the 16-row one; the
+// other parts' hi / lo values then come from lanes i + 16 p / kRep of the same 16-lane
+// row (DPP).  A rows past the batch hold other rows' values (their D rows are never
+// stored), and every stored result follows the same arithmetic whatever kRep (bitwise
+// identical for any batch size).
+template <int kFmt, int T, int W, int kNW, int kRep>
 __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __restrict__ w0,
                                                             const uint8_t* __restrict__ w1,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int n_rows, int n_tiles, int groups, int k, int batch) {
+    static_assert(kRep == 1 || kRep == 2 || kRep == 4, "lanes per activation row");
     constexpr int kNT = kNW * T;  // (weight, tile) pairs of the workgroup
+    constexpr int kXB = 4 / kRep;  // blocks of a group a lane loads and splits
+    constexpr int kPartRows = 16 / kRep;  // A rows per part: the batch rows
     using F = BFmt<kFmt>;
+    using St = Stage<kFmt, kNT, kXB>;
     constexpr int kCB = F::kCB;
     constexpr int kCodeBytes = kTileEntries * kCB;
     constexpr int kChunk = F::kChunk;
@@ -207,10 +249,15 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     uint32_t tile_off[T];
 #pragma unroll
     for (int i = 0; i < T; ++i) tile_off[i] = (uint32_t)min(tile0 + i, n_tiles - 1) * groups * kChunk;
-    // x: one buffer of batch * k floats; A row li reads batch row min(li, batch - 1)
-    // (rows past the batch are computed and not stored); elements past k read zero.
+    // x: one buffer of batch * k floats.  A row li carries batch row
+    // min(li % kPartRows, batch - 1) (rows past the batch are computed and not stored);
+    // the lane's blocks of a group start kXB * 32 * part elements in.  Elements past k
+    // read zero: k is a multiple of 32, so a block is in range iff its first element is.
+    const int part = li / kPartRows;
     const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x, (uint32_t)batch * (uint32_t)k * 4u);
-    const uint32_t x_row = (uint32_t)min(li, batch - 1) * (uint32_t)k;
+    const uint32_t x_lane =
+        ((uint32_t)min(li % kPartRows, batch - 1) * (uint32_t)k + (uint32_t)(part * kXB * 32 + kq * 8)) * 4u;
+    const int x_lim = k - part * kXB * 32;  // slot element offset g * 128 + 32 tt must be below
     float* my_scale = lds + wave * 16;
 
     f32x4 acc[kNT];
@@ -218,15 +265,15 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     for (int i = 0; i < kNT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // Issue group g's loads: activations first (L2 hits), then the chunks.
-    auto load = [&](Stage<kFmt, kNT>& st, int g) {
+    auto load = [&](St& st, int g) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t e = (uint32_t)g * 128u + t * 32u + kq * 8u;
-            const uint32_t off = e < (uint32_t)k ? (x_row + e) * 4u : 0x80000000u;
+        for (int tt = 0; tt < kXB; ++tt) {
+            const int ge = g * 128 + tt * 32;
+            const uint32_t off = x_lane + (ge < x_lim ? (uint32_t)ge * 4u : 0x80000000u);
             const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off, 0, 0));
             const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off + 16u, 0, 0));
-            st.x[t][0] = a.x; st.x[t][1] = a.y; st.x[t][2] = a.z; st.x[t][3] = a.w;
-            st.x[t][4] = b.x; st.x[t][5] = b.y; st.x[t][6] = b.z; st.x[t][7] = b.w;
+            st.x[tt][0] = a.x; st.x[tt][1] = a.y; st.x[tt][2] = a.z; st.x[tt][3] = a.w;
+            st.x[tt][4] = b.x; st.x[tt][5] = b.y; st.x[tt][6] = b.z; st.x[tt][7] = b.w;
         }
 #pragma unroll
         for (int i = 0; i < kNT; ++i) {
@@ -250,19 +297,34 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
 
     // One group: the range scale and hi / lo split of the activations (shared by the
     // kNT pairs), then per pair 4 blocks of 2 MFMAs and the scale FMAs.
-    auto compute = [&](const Stage<kFmt, kNT>& st) {
+    auto compute = [&](const St& st) {
         float m = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < kXB; ++tt)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(st.x[t][j]));
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(st.x[tt][j]));
         m = quarter_max(m);
+        if constexpr (kRep >= 2) m = fmaxf(m, row_ror<8>(m));  // the parts of a row: lanes li, li ^ 8
+        if constexpr (kRep == 4) m = fmaxf(m, row_ror<4>(m));  // and li + 4, li + 12
         // 2^e <= m < 2^(e+1), e = biased exponent - 127; s = 14 - e
         const int sh = 141 - (int)(__float_as_uint(m) >> 23);
         if (kq == 0) my_scale[li] = __builtin_amdgcn_ldexpf(1.0f, -sh);
-        f16x8 ah[4], al[4];
+        f16x8 ah[4], al[4];  // A operands of blocks 0..3 for the batch rows' lanes
 #pragma unroll
-        for (int t = 0; t < 4; ++t) split8(st.x[t], sh, ah[t], al[t]);
+        for (int tt = 0; tt < kXB; ++tt) split8(st.x[tt], sh, ah[tt], al[tt]);
+#pragma unroll
+        for (int t = kXB; t < 4; ++t) {  // part t / kXB: lanes li + kPartRows * (t / kXB)
+            if (t / kXB == 1) {
+                ah[t] = from_lane<kPartRows>(ah[t % kXB]);
+                al[t] = from_lane<kPartRows>(al[t % kXB]);
+            } else if (t / kXB == 2) {
+                ah[t] = from_lane<2 * kPartRows>(ah[t % kXB]);
+                al[t] = from_lane<2 * kPartRows>(al[t % kXB]);
+            } else {
+                ah[t] = from_lane<3 * kPartRows>(ah[t % kXB]);
+                al[t] = from_lane<3 * kPartRows>(al[t % kXB]);
+            }
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -336,7 +398,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     };
 
     if (g0 < g1) {  // uniform per wave
-        Stage<kFmt, kNT> sa, sb;
+        St sa, sb;
         int g = g0;
         load(sa, g);
         // the loads past the slice end re-read its last group (cache hits) and are
@@ -359,7 +421,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     for (int i = 0; i < kNT; ++i)
         *reinterpret_cast<f32x4*>(lds + ((wave * kNT + i) * 64 + lane) * 4) = acc[i];
     __syncthreads();
-    // output (tile i, batch row b, weight row r): lane (b / 4) * 16 + r, register b % 4
+    // output (tile i, batch row b): lane (b / 4) * 16 + r, register b % 4
     for (int f = (int)threadIdx.x; f < T * 256; f += 64 * W) {
         const int i = f >> 8, b = (f >> 4) & 15, r = f & 15;
         const int row = (tile0 + i) * kTileRows + r;
@@ -379,11 +441,11 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     }
 }
 
-template <int kFmt, int T, int W, int kNW>
+template <int kFmt, int T, int W, int kNW, int kRep>
 hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch, hipStream_t s) {
     const unsigned wgs = (unsigned)((w.n_tiles + T - 1) / T);
-    hipLaunchKernelGGL((gemv_batch_kernel<kFmt, T, W, kNW>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x, y,
-                       (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch);
+    hipLaunchKernelGGL((gemv_batch_kernel<kFmt, T, W, kNW, kRep>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x,
+                       y, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch);
     return hipGetLastError();
 }
 
@@ -427,7 +489,6 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 // 30.7 -> 25.2 us, Q4_K B = 16 31.9 -> 22.5 us, 28672 x 8192 Q4_0 B = 16 118 -> 80 us.
 constexpr int64_t kCUs = 256;  // MI355X compute units
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
-    (void)batch;
     BatchShape sh{};
     // a pair holds two weights' registers per tile: at most 4 / 3 tiles
     const bool nib = w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K;
@@ -435,15 +496,16 @@ BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     const int64_t per_cu = (w.n_tiles + kCUs - 1) / kCUs;
     sh.t = (int)(per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu);
     sh.w = w.groups >= 8 ? 4 : 1;
+    sh.rep = batch <= 4 ? 4 : batch <= 8 ? 2 : 1;
     return sh;
 }
 
-template <int kFmt, int kNW>
+template <int kFmt, int kNW, int kRep>
 static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
                                  const BatchShape& sh, hipStream_t s) {
 #define QMM_BATCH_CASE(T_)                                                                     \
-    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW>(w, w1, x, y, batch, s)          \
-                                     : run<kFmt, T_, 1, kNW>(w, w1, x, y, batch, s);
+    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW, kRep>(w, w1, x, y, batch, s)    \
+                                     : run<kFmt, T_, 1, kNW, kRep>(w, w1, x, y, batch, s);
     if (sh.w != 1 && sh.w != 4) return hipErrorInvalidValue;
     QMM_BATCH_CASE(1)
     QMM_BATCH_CASE(2)
@@ -467,6 +529,18 @@ static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float
     return hipErrorInvalidValue;
 }
 
+template <int kFmt, int kNW>
+static hipError_t dispatch_rep(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
+                               const BatchShape& sh, hipStream_t s) {
+    if (batch * sh.rep > kBatchRows) return hipErrorInvalidValue;  // 16 / rep batch rows per part
+    switch (sh.rep) {
+    case 1: return dispatch_batch<kFmt, kNW, 1>(w, w1, x, y, batch, sh, s);
+    case 2: return dispatch_batch<kFmt, kNW, 2>(w, w1, x, y, batch, sh, s);
+    case 4: return dispatch_batch<kFmt, kNW, 4>(w, w1, x, y, batch, sh, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, float* y, int batch,
                              const BatchShape& sh, hipStream_t s) {
     if (batch < 1 || batch > kBatchRows) return hipErrorInvalidValue;
@@ -474,17 +548,17 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
     const uint8_t* w1 = up ? up->chunks : nullptr;
     switch (w.type) {
     case OPENMINI_QMM_Q4_0:
-        return up ? dispatch_batch<OPENMINI_QMM_Q4_0, 2>(w, w1, x, y, batch, sh, s)
-                  : dispatch_batch<OPENMINI_QMM_Q4_0, 1>(w, w1, x, y, batch, sh, s);
+        return up ? dispatch_rep<OPENMINI_QMM_Q4_0, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q4_0, 1>(w, w1, x, y, batch, sh, s);
     case OPENMINI_QMM_Q8_0:
-        return up ? dispatch_batch<OPENMINI_QMM_Q8_0, 2>(w, w1, x, y, batch, sh, s)
-                  : dispatch_batch<OPENMINI_QMM_Q8_0, 1>(w, w1, x, y, batch, sh, s);
+        return up ? dispatch_rep<OPENMINI_QMM_Q8_0, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q8_0, 1>(w, w1, x, y, batch, sh, s);
     case OPENMINI_QMM_Q4_K:
-        return up ? dispatch_batch<OPENMINI_QMM_Q4_K, 2>(w, w1, x, y, batch, sh, s)
-                  : dispatch_batch<OPENMINI_QMM_Q4_K, 1>(w, w1, x, y, batch, sh, s);
+        return up ? dispatch_rep<OPENMINI_QMM_Q4_K, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q4_K, 1>(w, w1, x, y, batch, sh, s);
     case OPENMINI_QMM_Q6_K:
-        return up ? dispatch_batch<OPENMINI_QMM_Q6_K, 2>(w, w1, x, y, batch, sh, s)
-                  : dispatch_batch<OPENMINI_QMM_Q6_K, 1>(w, w1, x, y, batch, sh, s);
+        return up ? dispatch_rep<OPENMINI_QMM_Q6_K, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q6_K, 1>(w, w1, x, y, batch, sh, s);
     default: return hipErrorInvalidValue;
     }
 }

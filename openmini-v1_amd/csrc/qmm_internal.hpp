@@ -164,8 +164,10 @@ hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int coun
                              bool swiglu, hipStream_t s);
 
 // Batches of at least kBatchMin rows use the batched GEMV (qmm_gemv_batch.hip): from
-// five rows on, one pass over W beats the single-row kernel's launches of four rows.
-constexpr int kBatchMin = 5;
+// four rows on, one pass over W beats the single-row kernel (MI355X, b = 4: Q4_0
+// 11008 x 4096 11.6 vs 14.0 us, 28672 x 8192 40 vs 50 us, Q8_0 4096 x 11008 16.0-16.9 vs
+// 18.7 us; b = 3 is even and b = 2 favours the single-row kernel, 8.5 vs 11.0 us).
+constexpr int kBatchMin = 4;
 bool use_batch_kernel(const Weight& w, int64_t batch);
 
 // y[batch][n] = x[batch][k] . W^T for any batch >= 1 (with `up`: the SwiGLU pair as in
@@ -176,6 +178,7 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 // Batched GEMV (qmm_gemv_batch.hip): T row tiles per workgroup, W waves splitting K.
 struct BatchShape {
     int t = 1, w = 8;
+    int rep = 1;  // lanes per activation row: 1, 2 or 4 (batches of at most 16 / rep rows)
 };
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair);
 

@@ -242,18 +242,19 @@ def _adversarial_rows(w_f32, K, seed):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
-@pytest.mark.parametrize("B", [4, 8])
+@pytest.mark.parametrize("B", [3, 4, 8, 16])
 def test_gemv_error_within_fp32_path(qmm, orc, qtype, B):
     """The activation arithmetic is not narrower than the reference's f32 path: on
     adversarial rows, the largest error of each output row against the fp64 oracle is
     at most 4x that of the f32 GEMV over the dequantized weights (the reference's
-    per-token path, oracle.cpu_asrun_linear).  B = 4 runs the single-row kernel
-    (30-bit block-floating activations), B = 8 the batched one (fp16 hi / lo split)."""
+    per-token path, oracle.cpu_asrun_linear).  B = 3 runs the single-row kernel
+    (30-bit block-floating activations); B = 4, 8 and 16 the batched one (fp16 hi / lo
+    split) with 4, 2 and 1 lanes per activation row."""
     N, K = 512, 4096
     blocks = _zero_column(qtype, synth.weight_blocks(qtype, N, K, seed=0xAD0 + qtype), N, K, 5)
     w_f32 = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
     assert np.all(w_f32[:, 5] == 0.0)
-    x = _adversarial_rows(w_f32, K, 0xAD1)
+    x = _adversarial_rows(w_f32, K, 0xAD1)[:B]
     if B > 4:
         x = np.concatenate([x, synth.normal(0xAD2, (B - 4, K), 1.0)])
     wq = qmm.QuantizedWeight(qtype, blocks, N, K)
@@ -264,7 +265,8 @@ def test_gemv_error_within_fp32_path(qmm, orc, qtype, B):
         e_gpu = float(np.max(np.abs(y[r] - ref[r])))
         e_f32 = float(np.max(np.abs(y32[r] - ref[r])))
         print(f"row {r}: gpu {e_gpu:.3e} f32 path {e_f32:.3e}")
-        assert e_gpu <= 4.0 * e_f32, (r, e_gpu, e_f32)
+        if r < 4:  # the adversarial rows; the N(0, 1) filler rows only fill the batch
+            assert e_gpu <= 4.0 * e_f32, (r, e_gpu, e_f32)
         assert_parity(y[r:r + 1], ref[r:r + 1], TOL, f"row {r}")
 
 

@@ -1,4 +1,4 @@
-"""Batched decode GEMV (five or more activation rows: one pass over W on fp16 MFMA)
+"""Batched decode GEMV (four or more activation rows: one pass over W on fp16 MFMA)
 against the fp64 oracle (model.rs:1050-1064 semantics: y = x . W^T), tolerance from
 tests/parity.py (1e-3 normwise and elementwise)."""
 import numpy as np
@@ -21,7 +21,7 @@ def run_gemv(qmm, w, x):
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 @pytest.mark.parametrize("N,K", [(1, 32), (37, 96), (130, 2080), (255, 4064), (1000, 4000), (4096, 4096)])
-@pytest.mark.parametrize("B", [5, 8, 16, 21, 40])
+@pytest.mark.parametrize("B", [4, 5, 8, 16, 21, 36])
 def test_batch_parity(qmm, orc, qtype, N, K, B):
     print(f"gemv batch type={qtype} N={N} K={K} B={B}", flush=True)
     blocks = synth.weight_blocks(qtype, N, K, seed=0xB000 + N + K + B)
@@ -71,20 +71,25 @@ def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
     assert_parity(dy.download(np.float32, (B, N)), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} B={B}")
 
 
-@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, 12, 14])
 def test_batch_rows_independent(qmm, qtype):
-    """A row's result does not depend on the other rows of the batch (each MFMA row
-    and each range scale belongs to one activation row): rows 8..15 of a 16-row call
-    equal an 8-row call of the same rows bit for bit, and a repeated call is bitwise
-    identical."""
+    """A row's result depends neither on the other rows of the batch (each MFMA row
+    and each range scale belongs to one activation row) nor on the batch size: batches
+    of up to 8 and up to 4 rows split each row's activations over 2 and 4 lanes, and
+    their results must equal the 16-row kernel's bit for bit.  Rows 8..15 of a 16-row
+    call equal an 8-row call of the same rows, rows 0..3 a 4-row call, rows 4..9 a
+    6-row call; a repeated call is bitwise identical."""
     N, K = 777, 2048
-    blocks = synth.weight_blocks(qtype, N, K, seed=0xB200)
+    blocks = (synth.kquant_blocks(qtype, N, K, seed=0xB200) if qtype in (12, 14)
+              else synth.weight_blocks(qtype, N, K, seed=0xB200))
     w = qmm.QuantizedWeight(qtype, blocks, N, K)
     x = synth.normal(0xB201, (16, K), 1.0)
     x[3] *= 1e6  # a loud neighbour must not change the quiet rows
+    x[9, 100] = np.float32(1e-41)
     y16 = run_gemv(qmm, w, x)
-    y8 = run_gemv(qmm, w, x[8:])
-    assert np.array_equal(y16[8:].view(np.uint32), y8.view(np.uint32))
+    for lo, hi in ((8, 16), (0, 4), (4, 10), (12, 16)):
+        print(f"rows {lo}..{hi - 1} of 16 vs a {hi - lo}-row call", flush=True)
+        assert np.array_equal(y16[lo:hi].view(np.uint32), run_gemv(qmm, w, x[lo:hi]).view(np.uint32)), (lo, hi)
     assert np.array_equal(y16.view(np.uint32), run_gemv(qmm, w, x).view(np.uint32))
 
 

@@ -110,7 +110,7 @@ def test_q4_k_nonfinite_dmin_poisons_its_rows(qmm, orc):
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
 def test_kquant_layer_calls(qmm, orc, qtype):
     """gemv_multi (q / k / v sharing x) and the FFN hidden state silu(gate) * up on
-    K-quant weights, at batch 1 and at batch 6 (routed to launches of up to 4 rows)."""
+    K-quant weights, at batch 1 (single-row kernel) and at batch 6 (batched kernel)."""
     H, F = 512, 1280
     bq, bk = synth.kquant_blocks(qtype, H, H, 0xC400), synth.kquant_blocks(qtype, 256, H, 0xC401)
     bg, bu = synth.kquant_blocks(qtype, F, H, 0xC402), synth.kquant_blocks(qtype, F, H, 0xC403)
