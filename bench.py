@@ -39,6 +39,10 @@ BF16_PEAK_TFLOPS = 2500.0
 Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 12, 14
 TYPE_NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
 MALL_DEFEAT_BYTES = 1 << 30
+# the Llama-70B-style q / gate / down projections (N, K, seed),
+# weights N(0, 0.015)
+SHAPES_70B = ((8192, 8192, 0x5EED0064), (28672, 8192, 0x5EED0065), (8192, 28672, 0x5EED0066))
+SIGMA_70B = 0.015
 
 
 def sha256(a: np.ndarray) -> str:
@@ -80,10 +84,23 @@ def time_steps(launch, steps: int, stream, hipr) -> float:
     return e0.elapsed_ms(e1)
 
 
-def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed=0x5EED0001):
+_BLOCKS = {}
+
+
+def weight_blocks(qtype, N, K, seed, sigma=0.02):
+    """Synthetic GGUF blocks of W[N, K] ~ N(0, sigma), generated once per process for
+    the legs that share a weight (the 70B shapes at several batch sizes)."""
     from openmini_qmm import synth
-    blocks = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
-              else synth.weight_blocks(qtype, N, K, seed=seed))
+    key = (qtype, N, K, seed, sigma)
+    if key not in _BLOCKS:
+        _BLOCKS[key] = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
+                        else synth.weight_blocks(qtype, N, K, seed=seed, sigma=sigma))
+    return _BLOCKS[key]
+
+
+def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed=0x5EED0001, sigma=0.02):
+    from openmini_qmm import synth
+    blocks = weight_blocks(qtype, N, K, seed, sigma)
     wbytes = blocks.size  # GGUF bytes: the algorithmic weight bytes
     copies = max(2, -(-MALL_DEFEAT_BYTES // wbytes))
     log(f"gemv type={qtype} N={N} K={K} B={batch}: {copies} weight copies x {wbytes} B")
@@ -123,10 +140,10 @@ def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed
     return res
 
 
-def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q8_0, seed=0x5EED0003):
+def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q8_0, seed=0x5EED0003,
+               sigma=0.02):
     from openmini_qmm import synth
-    blocks = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
-              else synth.weight_blocks(qtype, N, K, seed=seed))
+    blocks = weight_blocks(qtype, N, K, seed, sigma)
     copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // blocks.size))
     log(f"gemm type={qtype} N={N} K={K} M={M}: {copies} weight copies")
     ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
@@ -551,6 +568,14 @@ def main(argv=None) -> int:
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                             "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
             log(f"{TYPE_NAME[qtype]} gemm M=512: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
+        # the 70B q / gate / down projections at prefill M = 1024
+        for n, k, seed in SHAPES_70B:
+            r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 10), max(3, args.warmup // 4), N=n, K=k,
+                           M=1024, qtype=Q4_0, seed=seed, sigma=SIGMA_70B)
+            prefill.append({"workload": f"q4_0_gemm_n{n}_k{k}_m1024_bf16x", "unit": "TFLOP/s",
+                            "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
+            log(f"q4_0 gemm {n}x{k} M=1024: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
     layer = None
     if not args.no_layer:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
@@ -558,10 +583,13 @@ def main(argv=None) -> int:
             f"separate {layer['separate_us']:.2f} us ({layer['separate_gbs']:.1f} GB/s)")
     batched = []
     if not args.no_batch:
-        # BASELINE configs[1] (Q8_0, batch 8) and configs[4] (70B gate, batch 16)
-        for qtype, n, k, b, seed in ((Q8_0, 11008, 4096, 8, 0x5EED0011), (Q4_0, 28672, 8192, 16, 0x5EED0041)):
+        # BASELINE configs[1] (Q8_0 up / down, batch 8) and configs[4] (70B q / gate / down,
+        # batch 4 and 16); the 70B legs share their weights with the batch-1 legs below
+        legs = [(Q8_0, 11008, 4096, 8, 0x5EED0011, 0.02), (Q8_0, 4096, 11008, 8, 0x5EED0012, 0.02)]
+        legs += [(Q4_0, n, k, b, seed, SIGMA_70B) for n, k, seed in SHAPES_70B for b in (4, 16)]
+        for qtype, n, k, b, seed, sigma in legs:
             r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
-                           qtype=qtype, batch=b, seed=seed)
+                           qtype=qtype, batch=b, seed=seed, sigma=sigma)
             name = "q4_0" if qtype == Q4_0 else "q8_0"
             batched.append({"workload": f"{name}_gemv_n{n}_k{k}_b{b}", "unit": "GB/s",
                             "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
@@ -571,11 +599,12 @@ def main(argv=None) -> int:
     shapes = []
     if not args.no_shapes:
         # the remaining decode configs of the measurement table (batch 1)
-        for qtype, n, k, seed in ((Q4_0, 4096, 4096, 0x5EED0061), (Q8_0, 11008, 4096, 0x5EED0062),
-                                  (Q8_0, 4096, 11008, 0x5EED0063), (Q4_0, 8192, 8192, 0x5EED0064),
-                                  (Q4_0, 28672, 8192, 0x5EED0065), (Q4_0, 8192, 28672, 0x5EED0066)):
+        legs = [(Q4_0, 4096, 4096, 0x5EED0061, 0.02), (Q8_0, 11008, 4096, 0x5EED0062, 0.02),
+                (Q8_0, 4096, 11008, 0x5EED0063, 0.02)]
+        legs += [(Q4_0, n, k, seed, SIGMA_70B) for n, k, seed in SHAPES_70B]
+        for qtype, n, k, seed, sigma in legs:
             r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
-                           qtype=qtype, batch=1, seed=seed)
+                           qtype=qtype, batch=1, seed=seed, sigma=sigma)
             name = "q4_0" if qtype == Q4_0 else "q8_0"
             shapes.append({"workload": f"{name}_gemv_n{n}_k{k}_b1", "unit": "GB/s",
                            "value": round(r["gbs_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
