@@ -78,6 +78,19 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
     return v;
 }
 
+// Sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), in every
+// lane, with the gfx950 row swaps (registers only, no LDS round trip).  Each step adds
+// the same two values in every lane of a row pair, so the result is the one of
+// v + v[l ^ 16], then + [l ^ 32].
+__device__ __forceinline__ float sum_rows(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // rows (0, 0, 2, 2), (1, 1, 3, 3)
+    const float w = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const uint32_t x = __float_as_uint(w);
+    const auto q = __builtin_amdgcn_permlane32_swap(x, x, false, false);  // rows (0, 1, 0, 1), (2, 3, 2, 3)
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // v_cvt_i32_f32: float -> int32, toward zero, saturating (NaN -> 0).  Written out
 // because a C++ conversion of a non-finite or out-of-range float is undefined.
 __device__ __forceinline__ int cvt_i32(float v) {
@@ -374,9 +387,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
     for (int nw = 0; nw < kNW; ++nw)
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            float v = acc[nw][b];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
+            float v = sum_rows(acc[nw][b]);
             if (bad[b]) v = __builtin_nanf("");
             if (lane < 16) red[wave][nw][b][lane] = v;
         }
