@@ -14,12 +14,12 @@
 //     Q6_K's scale changes every 16 elements, inside one MFMA's 32: each half runs its
 //     own MFMA pair with the other half's codes zeroed, scaled by its own factor.
 //   * Per (batch row, 4-block group) the activations are scaled by 2^s, s chosen so
-//     the group's largest |x| lands in [2^14, 2^15), and split exactly into
-//     hi = x' with its low 13 mantissa bits cleared (11 significant bits, an fp16
-//     value) and lo = x' - hi (at most 13 bits, rounded toward zero to fp16: a
-//     relative error below 2^-20 of the element; elements below 2^-14 of the group
-//     maximum lose bits only below 2^-38 of it).  The scale is a range guard: fp16
-//     cannot hold the full fp32 exponent range.
+//     the group's largest |x| lands in [2^14, 2^15), and split into hi = x' rounded
+//     toward zero to fp16 (11 significant bits: x' with its low 13 mantissa bits
+//     cleared) and lo = x' - hi, exact in fp32, rounded toward zero to fp16 (at most
+//     13 bits: a relative error below 2^-20 of the element; elements below 2^-14 of
+//     the group maximum lose bits only below 2^-38 of it).  The scale is a range
+//     guard: fp16 cannot hold the full fp32 exponent range.
 //   * v_mfma_f32_16x16x32_f16 covers one 32-element block: D = (hi + lo) . q in fp32
 //     for 16 batch rows x 16 weight rows.  Each block's D is scaled by its fp16 scale
 //     into a group sum; each group sum by 2^-s into the row's accumulator.
@@ -32,10 +32,11 @@
 // or bytes 8 kq .. 8 kq + 7 (Q8_0).  A chunk arrives as in the single-row kernel --
 // lane l reads slot l whole, one 1 KB (Q4_0) / 2 KB (Q8_0) wave load plus its 128 B
 // of scales -- and a 4 x 4 register transpose across the wave's four 16-lane rows
-// (row swaps, no LDS) hands every lane its words of all four blocks.  Vector-memory
-// instructions are what limits this kernel (each costs the address unit about the
-// same whatever its width), so wide loads and register shuffles beat narrow loads.
-// D: lane l holds column l % 16, rows 4 (l / 16) .. + 3.
+// (row swaps, no LDS) hands every lane its words of all four blocks: one wide load per
+// chunk costs the address unit what one narrow load would.  Batches of at most 8 or 4
+// rows leave A rows free; there 2 or 4 lanes share an activation row (kRep, below).
+// D: lane l holds column l % 16, rows 4 (l / 16) .. + 3.  VALU issue (code
+// conversion, scale FMAs, the activation split) is what bounds the kernel.
 //
 // Work split: a workgroup owns T consecutive row tiles (of kNW weights: a (gate, up)
 // pair runs both on the same tiles and writes silu(gate) * up, model.rs:713-735 with
