@@ -158,6 +158,15 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
  * batched kernel, one pass over W per 16 rows, in which a row's result does not
  * depend on the other rows of the call nor on the batch size (bitwise).  Every
  * weight type.
+ * A weight of at most 8192 rows and K >= 4000 splits K of a batched call over two or
+ * four workgroups per row tile; their partial sums and arrival counters live in a
+ * workspace after the weight's chunks (counted in device_bytes: 128 or 256 B per
+ * row plus one word per tile group).  Batched calls (4+ rows, here and in
+ * openmini_qmm_gemv_multi) on one such weight must therefore not overlap in time
+ * (two streams with no ordering between them): they would share the workspace.
+ * openmini_qmm_linear_host / _noalloc serialise their own such calls per weight.
+ * Calls of up to 3 rows, the SwiGLU pair and calls on different weights share no
+ * state.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);
@@ -172,9 +181,9 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
 /* ---- projections of one layer (src/model/inference/model.rs) ----------------------- */
 
 /* Weights that share the input: d_ys[i][batch, N_i] = x[batch, K] . W_i^T for
- * i < count (1..4), all of one type and one K; one launch per 4 batch rows, or from
- * 5 rows on one batched pass per weight (results identical to openmini_qmm_gemv of
- * each weight).  Replaces the three linear_gemm calls of prepare_qkv
+ * i < count (1..4), all of one type and one K; one launch for up to 3 batch rows,
+ * or from 4 rows on one batched pass per weight (results identical to
+ * openmini_qmm_gemv of each weight).  Replaces the three linear_gemm calls of prepare_qkv
  * (model.rs:1392-1394: q, k, v of one normalised hidden state).  d_x must be
  * 16-byte aligned. */
 int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count, const float* d_x,
@@ -183,7 +192,7 @@ int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count,
 /* FFN hidden state of FFNWeights::forward (model.rs:728-731, the silu(gate) * up
  * branch; silu(v) = v / (1 + exp(-v)), model.rs:1187-1189):
  * d_h[batch, N] = silu(x . Wg^T) * (x . Wu^T), gate and up of one type and shape, one
- * launch reading both weights per 4 batch rows (per 16 rows from 5 rows on).  d_x
+ * launch reading both weights for up to 3 batch rows (per 16 rows from 4 rows on).  d_x
  * must be 16-byte aligned. */
 int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qweight_t* up,
                              const float* d_x, float* d_h, int64_t batch, void* stream);

@@ -16,6 +16,11 @@
 
 struct openmini_qweight {
     qmm::Weight w;
+    // Serialises the synchronous host-memory calls of 4+ rows on a weight with a K
+    // split workspace, so concurrent host threads may share one handle there (their
+    // launches go to the null stream, which orders them too; the lock keeps that
+    // guarantee independent of the stream).
+    mutable std::mutex batch_mu;
 };
 
 namespace {
@@ -159,7 +164,10 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     w.n_tiles = (w.n + qmm::kTileRows - 1) / qmm::kTileRows;
     w.groups = (w.nb + qmm::kTileBlocks - 1) / qmm::kTileBlocks;
     w.chunk_bytes = (size_t)qmm::chunk_bytes(type);
-    w.device_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256);
+    qmm::batch_split(type, w.n_tiles, w.groups, &w.split_t, &w.split_s);
+    const size_t chunks_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256);
+    const size_t ws_bytes = qmm::split_workspace_bytes(w.n_tiles, w.split_t, w.split_s);
+    w.device_bytes = chunks_bytes + ws_bytes;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, w.device_bytes);
     if (e != hipSuccess) {
@@ -168,6 +176,11 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
                     hipGetErrorString(e));
     }
     w.chunks = static_cast<uint8_t*>(base);
+    if (ws_bytes) {
+        w.split_part = reinterpret_cast<float*>(w.chunks + chunks_bytes);
+        w.split_cnt = reinterpret_cast<uint32_t*>(
+            w.chunks + chunks_bytes + (size_t)w.split_s * qmm::kBatchRows * (size_t)w.n_tiles * qmm::kTileRows * 4);
+    }
     *out = h;
     return OPENMINI_QMM_OK;
 }
@@ -501,6 +514,8 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
     if (!x || !y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
     const qmm::Weight& w = weight->w;
+    std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
+    if (w.split_s > 1 && qmm::use_batch_kernel(w, m)) lk.lock();
     const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
     void *dx = nullptr, *dy = nullptr;
     hipError_t e = hipMalloc(&dx, xb);
@@ -535,6 +550,8 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
     uint8_t* base = nullptr;
     rc = scratch_on_device(w.device, &base);
     if (rc != OPENMINI_QMM_OK) return rc;
+    std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
+    if (w.split_s > 1 && qmm::use_batch_kernel(w, m)) lk.lock();
     const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
     float* dx = reinterpret_cast<float*>(base);
     float* dy = reinterpret_cast<float*>(base + round_up(xb, 256));

@@ -44,7 +44,10 @@
 // them one group at a time, with the next group's loads (activations, then the chunks)
 // in flight while the current group is split (once for the T tiles) and multiplied.
 // The W partial sums of an output meet in LDS and are added in wave order
-// (deterministic).
+// (deterministic).  A weight of few row tiles also splits K over 2 or 4 workgroups per
+// tile group (batch_split): each stores its sums in the weight's workspace and counts
+// itself in; the last to arrive adds the splits' sums in split order, so the result
+// does not depend on which one finishes last.
 #include "qmm_internal.hpp"
 
 namespace qmm {
@@ -221,7 +224,9 @@ template <int kFmt, int T, int W, int kNW, int kRep>
 __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __restrict__ w0,
                                                             const uint8_t* __restrict__ w1,
                                                             const float* __restrict__ x, float* __restrict__ y,
-                                                            int n_rows, int n_tiles, int groups, int k, int batch) {
+                                                            int n_rows, int n_tiles, int groups, int k, int batch,
+                                                            float* __restrict__ sums, uint32_t* __restrict__ cnt,
+                                                            int splits) {
     static_assert(kRep == 1 || kRep == 2 || kRep == 4, "lanes per activation row");
     constexpr int kNT = kNW * T;  // (weight, tile) pairs of the workgroup
     constexpr int kXB = 4 / kRep;  // blocks of a group a lane loads and splits
@@ -240,9 +245,14 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 15, kq = lane >> 4;
-    const int tile0 = (int)blockIdx.x * T;
-    const int g0 = (int)((int64_t)groups * wave / W);
-    const int g1 = (int)((int64_t)groups * (wave + 1) / W);
+    // workgroup = (tile group, K split): the split's contiguous K groups [gs0, gs1)
+    const int split = (int)blockIdx.x % splits;
+    const int tgroup = (int)blockIdx.x / splits;
+    const int tile0 = tgroup * T;
+    const int gs0 = (int)((int64_t)groups * split / splits);
+    const int gsn = (int)((int64_t)groups * (split + 1) / splits) - gs0;
+    const int g0 = gs0 + (int)((int64_t)gsn * wave / W);
+    const int g1 = gs0 + (int)((int64_t)gsn * (wave + 1) / W);
 
     const __amdgpu_buffer_rsrc_t w_rs0 = make_rsrc(w0, (uint32_t)n_tiles * groups * kChunk);
     const __amdgpu_buffer_rsrc_t w_rs1 = make_rsrc(kNW == 2 ? w1 : w0, (uint32_t)n_tiles * groups * kChunk);
@@ -423,6 +433,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         *reinterpret_cast<f32x4*>(lds + ((wave * kNT + i) * 64 + lane) * 4) = acc[i];
     __syncthreads();
     // output (tile i, batch row b): lane (b / 4) * 16 + r, register b % 4
+    const size_t n_pad = (size_t)n_tiles * kTileRows;
     for (int f = (int)threadIdx.x; f < T * 256; f += 64 * W) {
         const int i = f >> 8, b = (f >> 4) & 15, r = f & 15;
         const int row = (tile0 + i) * kTileRows + r;
@@ -437,16 +448,50 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         }
         if constexpr (kNW == 2)
             y[(size_t)b * n_rows + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
-        else
+        else if (splits == 1)
             y[(size_t)b * n_rows + row] = v[0];
+        else  // device-coherent store (write-through past this XCD's L2)
+            __hip_atomic_store(sums + ((size_t)split * kBatchRows + b) * n_pad + row, v[0], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (kNW == 1) {
+        if (splits == 1) return;
+        // K split: the last of the tile group's workgroups to finish adds the splits'
+        // sums in split order (the same bits whichever finishes last) and resets the
+        // group's counter for the next call.  No workgroup waits for another.  The sums
+        // are stored and loaded as device-scope atomics, which write through and read
+        // past the per-XCD L2s, so no L2 write-back or invalidate (a device-scope fence)
+        // is needed: a workgroup counts itself only once its stores have completed
+        // (vmcnt 0), and the last one loads the sums only after its count returned.
+        __shared__ uint32_t last;
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cnt + tgroup, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(splits - 1);
+        __syncthreads();
+        if (!last) return;
+        for (int f = (int)threadIdx.x; f < T * 256; f += 64 * W) {
+            const int i = f >> 8, b = (f >> 4) & 15, r = f & 15;
+            const int row = (tile0 + i) * kTileRows + r;
+            if (b >= batch || tile0 + i >= n_tiles || row >= n_rows) continue;
+            const float* p = sums + (size_t)b * n_pad + row;
+            float v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int q = 1; q < splits; ++q)
+                v += __hip_atomic_load(p + (size_t)q * kBatchRows * n_pad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            y[(size_t)b * n_rows + row] = v;
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + tgroup, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 template <int kFmt, int T, int W, int kNW, int kRep>
-hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch, hipStream_t s) {
-    const unsigned wgs = (unsigned)((w.n_tiles + T - 1) / T);
+hipError_t run(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch, int splits,
+               hipStream_t s) {
+    const unsigned wgs = (unsigned)((w.n_tiles + T - 1) / T * splits);
     hipLaunchKernelGGL((gemv_batch_kernel<kFmt, T, W, kNW, kRep>), dim3(wgs), dim3(64 * W), 0, s, w.chunks, w1, x,
-                       y, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch);
+                       y, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k, batch, w.split_part, w.split_cnt,
+                       splits);
     return hipGetLastError();
 }
 
@@ -489,13 +534,60 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 // against one tile per workgroup, 11008 x 4096 Q4_0 B = 8 25.5 -> 20.8 us, Q8_0 B = 8
 // 30.7 -> 25.2 us, Q4_K B = 16 31.9 -> 22.5 us, 28672 x 8192 Q4_0 B = 16 118 -> 80 us.
 constexpr int64_t kCUs = 256;  // MI355X compute units
+
+static int64_t tiles_per_cu(int type, int64_t n_tiles, bool pair) {
+    // a pair holds two weights' registers per tile: at most 4 / 3 tiles
+    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K;
+    const int64_t cap = pair ? (nib ? 4 : 3) : nib ? 8 : 4;
+    const int64_t per_cu = (n_tiles + kCUs - 1) / kCUs;
+    return per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu;
+}
+
+// K split, measured on MI355X (three interleaved A/B passes on one box): at most 512
+// row tiles leave each workgroup 1 or 2 tiles to share its waves' activation split.
+// Two workgroups per tile group of twice the tiles, each over half of K, halve that
+// share: Q4_0 8192 x 28672 B = 16 60.8 -> 47.9 us, B = 4 45.6 -> 42.8; 8192 x 8192
+// B = 16 21.1 -> 18.7-20.0, B = 4 16.4 -> 16.3-17.0; 4096 x 11008 Q8_0 B = 8 18.3 ->
+// 16.0-16.9, Q4_0 B = 8 16.1 -> 14.3-14.9; 4096 x 4096 B = 16 10.5 -> 9.9.  Three or
+// four splits, or a split at 688 tiles (T = 6), were slower (258 workgroups for 256
+// CUs; 3-4 groups per wave).  At most 128 tiles fill at most half the CUs with one
+// tile per workgroup; there the K split alone fills them: 1024 x 8192 (64 tiles, 4
+// splits) Q4_0 B = 16 17.1 -> 10.0 us, B = 4 10.0 -> 7.8 us, Q8_0 B = 8 11.6 -> 8.4 us
+// (2 splits of 2 tiles: 12.9 us, 4 splits of 2 tiles 10.4 us at B = 16).  The choice
+// depends on the shape only, so results stay bitwise independent of the batch size.
+void batch_split(int type, int64_t n_tiles, int64_t groups, int* t, int* s) {
+    const int64_t t0 = tiles_per_cu(type, n_tiles, false);
+    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K;
+    *t = (int)t0;
+    *s = 1;
+    if (groups < 32) return;  // at least 16 groups per split
+    if (n_tiles <= kCUs / 4 && groups >= 64) {
+        *t = 1;
+        *s = 4;
+    } else if (n_tiles <= kCUs / 2) {
+        *t = 1;
+        *s = 2;
+    } else if (n_tiles <= 2 * kCUs && 2 * t0 <= (nib ? 8 : 4)) {
+        *t = (int)(2 * t0);
+        *s = 2;
+    }
+}
+
+size_t split_workspace_bytes(int64_t n_tiles, int t, int s) {
+    if (s <= 1) return 0;
+    const size_t part = (size_t)s * kBatchRows * (size_t)n_tiles * kTileRows * 4;
+    const size_t cnt = (size_t)((n_tiles + t - 1) / t) * 4;
+    return part + (cnt + 255) / 256 * 256;
+}
+
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     BatchShape sh{};
-    // a pair holds two weights' registers per tile: at most 4 / 3 tiles
-    const bool nib = w.type == OPENMINI_QMM_Q4_0 || w.type == OPENMINI_QMM_Q4_K;
-    const int64_t cap = pair ? (nib ? 4 : 3) : nib ? 8 : 4;
-    const int64_t per_cu = (w.n_tiles + kCUs - 1) / kCUs;
-    sh.t = (int)(per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu);
+    if (pair) {
+        sh.t = (int)tiles_per_cu(w.type, w.n_tiles, true);
+    } else {
+        sh.t = w.split_t;
+        sh.split = w.split_s;
+    }
     sh.w = w.groups >= 8 ? 4 : 1;
     sh.rep = batch <= 4 ? 4 : batch <= 8 ? 2 : 1;
     return sh;
@@ -504,9 +596,9 @@ BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
 template <int kFmt, int kNW, int kRep>
 static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
                                  const BatchShape& sh, hipStream_t s) {
-#define QMM_BATCH_CASE(T_)                                                                     \
-    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW, kRep>(w, w1, x, y, batch, s)    \
-                                     : run<kFmt, T_, 1, kNW, kRep>(w, w1, x, y, batch, s);
+#define QMM_BATCH_CASE(T_)                                                                          \
+    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW, kRep>(w, w1, x, y, batch, sh.split, s)   \
+                                     : run<kFmt, T_, 1, kNW, kRep>(w, w1, x, y, batch, sh.split, s);
     if (sh.w != 1 && sh.w != 4) return hipErrorInvalidValue;
     QMM_BATCH_CASE(1)
     QMM_BATCH_CASE(2)
@@ -546,6 +638,9 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
                              const BatchShape& sh, hipStream_t s) {
     if (batch < 1 || batch > kBatchRows) return hipErrorInvalidValue;
     if ((int64_t)batch * w.k * 4 > INT32_MAX) return hipErrorInvalidValue;  // 31-bit x offsets
+    // a K split runs on one weight, with the workspace sized for its tile groups
+    if (sh.split != 1 && (up || sh.split != w.split_s || sh.t != w.split_t || !w.split_part))
+        return hipErrorInvalidValue;
     const uint8_t* w1 = up ? up->chunks : nullptr;
     switch (w.type) {
     case OPENMINI_QMM_Q4_0:

@@ -142,13 +142,19 @@ struct Weight {
     uint8_t* chunks = nullptr;  // n_tiles * groups chunks, tile-major
     size_t chunk_bytes = 0;
     size_t device_bytes = 0;
+    // Batched-GEMV K split (split_s > 1, see batch_split): after the chunks, in the
+    // same allocation, split_s x kBatchRows x (n_tiles * 16) fp32 partial sums and one
+    // arrival counter per workgroup tile group (zero between calls).
+    int split_t = 1, split_s = 1;
+    float* split_part = nullptr;
+    uint32_t* split_cnt = nullptr;
     int64_t n_chunks() const { return n_tiles * groups; }
 };
 
 // ---- kernel launchers (qmm_repack.hip, qmm_gemv.hip, qmm_gemm.hip) ----------------
 
 // GGUF blocks (device, row-major [n][nb]) -> the chunks of `w`, every byte written
-// (the tile padding as zeros).
+// (the tile padding as zeros); clears the split counters of a weight that has them.
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s);
 
 // Repacked weight -> f32 [n][k].
@@ -178,9 +184,17 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 // Batched GEMV (qmm_gemv_batch.hip): T row tiles per workgroup, W waves splitting K.
 struct BatchShape {
     int t = 1, w = 8;
-    int rep = 1;  // lanes per activation row: 1, 2 or 4 (batches of at most 16 / rep rows)
+    int rep = 1;    // lanes per activation row: 1, 2 or 4 (batches of at most 16 / rep rows)
+    int split = 1;  // workgroups per tile group, each over 1 / split of K (one weight only)
 };
 BatchShape choose_batch_shape(const Weight& w, int batch, bool pair);
+
+// Tiles per workgroup (*t) and K splits (*s) of the batched kernel on one weight of
+// n_tiles row tiles and `groups` K groups; a weight with *s > 1 carries the split
+// workspace (Weight::split_part / split_cnt).
+void batch_split(int type, int64_t n_tiles, int64_t groups, int* t, int* s);
+// Bytes of that workspace (0 when s == 1).
+size_t split_workspace_bytes(int64_t n_tiles, int t, int s);
 
 // y[batch][n] = x[batch][k] . W^T for 1 <= batch <= kBatchRows in one pass over W; with
 // `up`, a (gate = w, up) pair of equal shape and y = silu(x . Wg^T) * (x . Wu^T).

@@ -562,9 +562,28 @@ inline unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)((items + per_block - 1) / per_block);
 }
 
+// Clears n words: the batched GEMV's split counters of a new weight, on the upload's
+// stream (a kernel rather than a memset node, so the upload may be graph-captured).
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) p[i] = 0;
+}
+
+hipError_t launch_repack_chunks(const Weight& w, const uint8_t* gguf, hipStream_t s);
+
 }  // namespace
 
 hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
+    const hipError_t e = launch_repack_chunks(w, gguf, s);
+    if (e != hipSuccess || !w.split_cnt) return e;
+    const int n = (int)((w.n_tiles + w.split_t - 1) / w.split_t);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, w.split_cnt, n);
+    return hipGetLastError();
+}
+
+namespace {
+
+hipError_t launch_repack_chunks(const Weight& w, const uint8_t* gguf, hipStream_t s) {
     if (w.n_tiles <= 0 || w.groups <= 0) return hipSuccess;
     if (is_kquant(w.type)) {
         const int64_t supers = w.k / 256;
@@ -592,6 +611,8 @@ hipError_t launch_repack(const Weight& w, const uint8_t* gguf, hipStream_t s) {
                            quads, aligned, w.chunks);
     return hipGetLastError();
 }
+
+}  // namespace
 
 hipError_t launch_dequant_weight(const Weight& w, float* out, hipStream_t s) {
     const int64_t nwords = w.n * w.nb * 4;

@@ -71,6 +71,75 @@ def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
     assert_parity(dy.download(np.float32, (B, N)), orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} B={B}")
 
 
+@pytest.mark.parametrize("qtype,N,K", [
+    (Q4_0, 1024, 8192),        # 64 tiles, 64 groups: 4 K splits of 1 tile
+    (Q4_0, 1030, 8192),        # 65 tiles (ragged): 2 splits of 1 tile
+    (Q8_0, 2000, 4096),        # 125 tiles, 32 groups: 2 splits of 1 tile
+    (12, 4096, 4096),          # Q4_K, 256 tiles: 2 splits of 2 tiles
+    (14, 4096, 4096),          # Q6_K, the same
+    (Q8_0, 8192, 4096),        # 512 tiles: 2 splits of 4 tiles
+    (Q4_0, 1024, 3968),        # 31 groups: no split
+])
+def test_batch_k_split(qmm, orc, qtype, N, K):
+    """The K-split launches (two or four workgroups per tile group, each over a part
+    of K; the last to finish adds the parts in split order and clears the group's
+    arrival counter).  Every call is checked on all outputs, y NaN-filled first:
+    against the oracle at 4, 7 and 16 rows, and bit for bit against a repeat of the
+    same call (a counter not cleared would leave outputs unwritten or half-summed)
+    and against the 16-row call's rows (the split depends on the shape only)."""
+    blocks = (synth.kquant_blocks(qtype, N, K, seed=0xB700 + N) if qtype in (12, 14)
+              else synth.weight_blocks(qtype, N, K, seed=0xB700 + N))
+    x16 = synth.normal(0xB701 + N, (16, K), 1.0)
+    x16[3] *= 1e4
+    w = qmm.QuantizedWeight(qtype, blocks, N, K)
+
+    def call(x):
+        B = x.shape[0]
+        dx, dy = qmm.DeviceBuffer.from_numpy(np.ascontiguousarray(x)), qmm.DeviceBuffer(B * N * 4)
+        dy.fill(0xFF)
+        w.gemv(dx, dy, B)
+        return dy.download(np.float32, (B, N))
+
+    y16 = call(x16)
+    for B in (4, 7, 16):
+        print(f"gemv batch k-split type={qtype} N={N} K={K} B={B}", flush=True)
+        y = call(x16[:B])
+        assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x16[:B]), TOL, f"N={N} K={K} B={B}")
+        assert np.array_equal(y.view(np.uint32), call(x16[:B]).view(np.uint32)), "repeat call differs"
+        assert np.array_equal(y.view(np.uint32), y16[:B].view(np.uint32)), f"B={B} rows differ from B=16"
+
+
+def test_engine_matmul_threads_share_a_split_weight(qmm):
+    """The engine's matmul (openmini_qmm_linear_host) on one K-split weight from four
+    host threads at once, 8 rows each (the batched kernel).  The calls run on the
+    null stream, shared by all host threads, and the library also serialises them
+    per weight; every thread's result must equal the single-threaded one bit for
+    bit."""
+    import threading
+    N, K = 1024, 8192  # 4 K splits
+    blocks = synth.weight_blocks(Q4_0, N, K, seed=0xB800)
+    w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
+    eng = qmm.get_gemm_engine()
+    xs = [synth.normal(0xB801 + t, (8, K), 1.0) for t in range(4)]
+    want = [eng.matmul(x, w) for x in xs]
+    got = [[] for _ in xs]
+
+    def worker(t):
+        for _ in range(6):
+            got[t].append(eng.matmul(xs[t], w))
+
+    print("gemv batch engine threads N=1024 K=8192 B=8", flush=True)
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    for t in range(4):
+        assert len(got[t]) == 6
+        for y in got[t]:
+            assert np.array_equal(y.view(np.uint32), want[t].view(np.uint32)), f"thread {t} differs"
+
+
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0, 12, 14])
 def test_batch_rows_independent(qmm, qtype):
     """A row's result depends neither on the other rows of the batch (each MFMA row
