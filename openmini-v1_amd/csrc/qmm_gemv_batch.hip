@@ -523,7 +523,11 @@ hipError_t launch_gemv_rows(const Weight& w, const Weight* up, const float* x, f
 }
 
 // Launch shape, measured on MI355X (Q4_0 / Q8_0 / Q4_K, B = 8, 16, N = 4096 ... 28672):
-// four waves per workgroup (one when K has fewer than 8 groups); tiles per workgroup
+// four waves per workgroup (one when K has fewer than 8 groups), eight (two per SIMD)
+// for one weight when a workgroup walks at least 64 K groups (three interleaved A/B
+// passes: Q4_0 28672 x 8192 B = 4 40.1-40.6 -> 38.6-39.0 us, B = 16 43.8-44.5 ->
+// 41.8-43.0, 8192 x 28672 (2 K splits) B = 4 42.3-43.0 -> 39.2-41.1, B = 16 even;
+// with 32-43 groups per workgroup eight waves lost up to 10%); tiles per workgroup
 // so that the grid is one workgroup per CU, all CUs busy: T = ceil(tiles / 256), at
 // most 8 (Q4_0 / Q4_K) or 4 (Q8_0 / Q6_K, whose 8-tile registers would leave one
 // wave per SIMD).  More tiles share each wave's activation loads and split; more
@@ -589,6 +593,8 @@ BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
         sh.split = w.split_s;
     }
     sh.w = w.groups >= 8 ? 4 : 1;
+    // at least 64 K groups per workgroup: eight waves of 8+ groups each (two per SIMD)
+    if (!pair && w.groups / sh.split >= 64) sh.w = 8;
     sh.rep = batch <= 4 ? 4 : batch <= 8 ? 2 : 1;
     return sh;
 }
@@ -597,9 +603,13 @@ template <int kFmt, int kNW, int kRep>
 static hipError_t dispatch_batch(const Weight& w, const uint8_t* w1, const float* x, float* y, int batch,
                                  const BatchShape& sh, hipStream_t s) {
 #define QMM_BATCH_CASE(T_)                                                                          \
-    if (sh.t == T_) return sh.w == 4 ? run<kFmt, T_, 4, kNW, kRep>(w, w1, x, y, batch, sh.split, s)   \
-                                     : run<kFmt, T_, 1, kNW, kRep>(w, w1, x, y, batch, sh.split, s);
-    if (sh.w != 1 && sh.w != 4) return hipErrorInvalidValue;
+    if (sh.t == T_) {                                                                               \
+        if constexpr (kNW == 1)                                                                     \
+            if (sh.w == 8) return run<kFmt, T_, 8, kNW, kRep>(w, w1, x, y, batch, sh.split, s);      \
+        return sh.w == 4 ? run<kFmt, T_, 4, kNW, kRep>(w, w1, x, y, batch, sh.split, s)             \
+                         : run<kFmt, T_, 1, kNW, kRep>(w, w1, x, y, batch, sh.split, s);            \
+    }
+    if (sh.w != 1 && sh.w != 4 && !(kNW == 1 && sh.w == 8)) return hipErrorInvalidValue;
     QMM_BATCH_CASE(1)
     QMM_BATCH_CASE(2)
     if constexpr (kNW == 2) {

@@ -79,11 +79,15 @@ def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
     (14, 4096, 4096),          # Q6_K, the same
     (Q8_0, 8192, 4096),        # 512 tiles: 2 splits of 4 tiles
     (Q4_0, 1024, 3968),        # 31 groups: no split
+    (Q8_0, 2000, 16384),       # 2 splits of 1 tile, 64 groups each: eight waves
+    (14, 4096, 16384),         # Q6_K, 2 splits of 2 tiles, eight waves
+    (12, 9600, 8192),          # Q4_K, 600 tiles (3 per workgroup), no split, eight waves
 ])
 def test_batch_k_split(qmm, orc, qtype, N, K):
     """The K-split launches (two or four workgroups per tile group, each over a part
     of K; the last to finish adds the parts in split order and clears the group's
-    arrival counter).  Every call is checked on all outputs, y NaN-filled first:
+    arrival counter), and the eight-wave workgroups of 64+ K groups.  Every call is
+    checked on all outputs, y NaN-filled first:
     against the oracle at 4, 7 and 16 rows, and bit for bit against a repeat of the
     same call (a counter not cleared would leave outputs unwritten or half-summed)
     and against the 16-row call's rows (the split depends on the shape only)."""
