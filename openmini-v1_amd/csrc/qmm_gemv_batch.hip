@@ -649,7 +649,7 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
     if (batch < 1 || batch > kBatchRows) return hipErrorInvalidValue;
     if ((int64_t)batch * w.k * 4 > INT32_MAX) return hipErrorInvalidValue;  // 31-bit x offsets
     // a K split runs on one weight, with the workspace sized for its tile groups
-    if (sh.split != 1 && (up || sh.split != w.split_s || sh.t != w.split_t || !w.split_part))
+    if (sh.split < 1 || (sh.split != 1 && (up || sh.split != w.split_s || sh.t != w.split_t || !w.split_part)))
         return hipErrorInvalidValue;
     const uint8_t* w1 = up ? up->chunks : nullptr;
     switch (w.type) {
