@@ -113,6 +113,41 @@ def test_batch_k_split(qmm, orc, qtype, N, K):
         assert np.array_equal(y.view(np.uint32), y16[:B].view(np.uint32)), f"B={B} rows differ from B=16"
 
 
+def test_k_split_graph_replays_match_eager(qmm):
+    """K-split batched GEMVs captured in a HIP graph, as a serving loop replays a
+    decode step.  Every replay must equal the eager result bit for bit. Eager calls
+    on the same weights run between the replays: each call must leave the split
+    counters at zero for the next, captured or not. No memset node is involved; the
+    counters are cleared by the kernels themselves."""
+    from openmini_qmm import hip_runtime as hipr
+    cases = [(Q4_0, 1024, 8192, 16), (Q8_0, 4096, 8192, 8), (Q4_0, 4096, 4096, 4)]
+    st = qmm.Stream()
+    sh = st.handle
+    runs = []
+    for qtype, N, K, B in cases:
+        blocks = synth.weight_blocks(qtype, N, K, seed=0xB900 + N + K)
+        w = qmm.QuantizedWeight(qtype, blocks, N, K)
+        dx = qmm.DeviceBuffer.from_numpy(synth.normal(0xB901 + N, (B, K), 1.0))
+        dx2 = qmm.DeviceBuffer.from_numpy(synth.normal(0xB902 + N, (B, K), 1.0))
+        dy, dy2 = qmm.DeviceBuffer(B * N * 4), qmm.DeviceBuffer(B * N * 4)
+        w.gemv(dx, dy, B, sh)
+        st.synchronize()
+        runs.append((w, dx, dx2, dy, dy2, B, N, dy.download(np.float32, (B, N))))
+    print("gemv batch k-split graph: capture", flush=True)
+    graph = hipr.Graph(sh, lambda s: [w.gemv(dx, dy, B, s) for w, dx, _, dy, _, B, _, _ in runs])
+    for rep in range(3):
+        print(f"gemv batch k-split graph: replay {rep}", flush=True)
+        for r in runs:
+            r[3].fill(0xFF, sh)
+        graph.launch(sh)
+        st.synchronize()
+        for w, dx, dx2, dy, dy2, B, N, want in runs:
+            got = dy.download(np.float32, (B, N))
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep} N={N} B={B}"
+            w.gemv(dx2, dy2, B, sh)  # eager work on the same weight between replays
+        st.synchronize()
+
+
 def test_engine_matmul_threads_share_a_split_weight(qmm):
     """The engine's matmul (openmini_qmm_linear_host) on one K-split weight from four
     host threads at once, 8 rows each (the batched kernel).  The calls run on the
