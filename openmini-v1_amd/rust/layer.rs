@@ -1,7 +1,9 @@
 //! One layer's projections with activations resident on the device (FFNWeights::forward,
 //! model.rs:713-735; prepare_qkv, model.rs:1379-1410).  A serving loop can capture a
 //! layer's launches once in a HIP graph on its stream and replay it per token: none of
-//! these calls allocates or sets memory.
+//! these calls allocates or sets memory.  Calls of 4+ rows on one weight of at most 8192
+//! rows share that weight's K-split workspace, so they must be ordered (one stream, or
+//! events between streams); a layer decoded on one stream satisfies that.
 use std::os::raw::c_void;
 
 use super::engine::HipQuantWeight;
