@@ -392,44 +392,57 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no copy may land after the stages are reused
 
     // ---- K parts meet in LDS (the stages are free after this barrier), then store.
+    // Parts 1.. hand their sums over as one 16-byte LDS write per subtile and lane;
+    // part 0 issues all its LDS reads together, adds the parts in order (fixed, so the
+    // bits do not depend on timing) and stores.
     __syncthreads();
-    float* red = reinterpret_cast<float*>(lds);
-    constexpr int kAcc = kMI * kWT * 4;  // accumulators per lane
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+    auto slot = [&](int h, int i, int j) { return ((((h - 1) * kNW + wn) * kMI + i) * kWT + j) * 64 + lane; };
     if (kh > 0) {
-        float* mine = red + ((size_t)(kh - 1) * kNW + wn) * kAcc * 64;
 #pragma unroll
         for (int i = 0; i < kMI; ++i)
 #pragma unroll
-            for (int j = 0; j < kWT; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) mine[((i * kWT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+            for (int j = 0; j < kWT; ++j) red[slot(kh, i, j)] = acc[i][j];
     }
     __syncthreads();
     if (kh == 0) {
-        const bool full_m = m0 + kBM <= m_rows;
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) {
-            const int gn = (tile0 + j) * kTileRows + li;
-            if (tile0 + j >= n_tiles || gn >= n_rows) continue;
-            float* yc = y + gn;
+        for (int h = 1; h < kKS; ++h) {
+            f32x4 part[kMI][kWT];  // all of a part's reads in flight before the first add
 #pragma unroll
             for (int i = 0; i < kMI; ++i)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // lane holds D[4 kq + r][li] of each 16 x 16 subtile; parts added in order
-                    float v = acc[i][j][r];
+                for (int j = 0; j < kWT; ++j) part[i][j] = red[slot(h, i, j)];
 #pragma unroll
-                    for (int h = 1; h < kKS; ++h)
-                        v += red[(((size_t)(h - 1) * kNW + wn) * kAcc + (i * kWT + j) * 4 + r) * 64 + lane];
-                    const int gm = m0 + i * 16 + kq * 4 + r;
-                    if (full_m || gm < m_rows) {
-                        if constexpr (kGate) {
-                            const float g = yc[(size_t)gm * n_rows];
-                            v = g / (1.0f + expf(-g)) * v;
-                        }
-                        yc[(size_t)gm * n_rows] = v;
-                    }
-                }
+            for (int i = 0; i < kMI; ++i)
+#pragma unroll
+                for (int j = 0; j < kWT; ++j) acc[i][j] += part[i][j];
+        }
+        // lane holds D[4 kq + r][li] of each 16 x 16 subtile
+        auto store = [&](int i, int j, int r) {
+            float* yp = y + (size_t)(m0 + i * 16 + kq * 4 + r) * n_rows + (tile0 + j) * kTileRows + li;
+            float v = acc[i][j][r];
+            if constexpr (kGate) {
+                const float g = *yp;
+                v = g / (1.0f + expf(-g)) * v;
+            }
+            *yp = v;
+        };
+        if (m0 + kBM <= m_rows && (tile0 + kWT) * kTileRows <= n_rows) {  // whole tile inside y
+#pragma unroll
+            for (int j = 0; j < kWT; ++j)
+#pragma unroll
+                for (int i = 0; i < kMI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) store(i, j, r);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kWT; ++j)
+#pragma unroll
+                for (int i = 0; i < kMI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (m0 + i * 16 + kq * 4 + r < m_rows && (tile0 + j) * kTileRows + li < n_rows) store(i, j, r);
         }
     }
 }
