@@ -47,6 +47,14 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+// Device code is written for gfx950 only: its instruction forms (row-swap permutes,
+// the gfx950 MFMA shapes, buffer loads to LDS) and the memory-ordering rules the
+// batched GEMV's K split relies on (gfx9's store-counting vmcnt, write-through
+// agent-scope stores) are those of this part.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "libopenmini_qmm device code targets gfx950 only (--offload-arch=gfx950)"
+#endif
 #include <stddef.h>
 #include <stdint.h>
 

@@ -85,12 +85,14 @@ def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
 ])
 def test_batch_k_split(qmm, orc, qtype, N, K):
     """The K-split launches (two or four workgroups per tile group, each over a part
-    of K; the last to finish adds the parts in split order and clears the group's
-    arrival counter), and the eight-wave workgroups of 64+ K groups.  Every call is
-    checked on all outputs, y NaN-filled first:
+    of K; the last to finish adds the parts in split order; the group's arrival
+    counter only grows, by the split count per call), and the eight-wave workgroups
+    of 64+ K groups.  Every call is checked on all outputs, y NaN-filled first:
     against the oracle at 4, 7 and 16 rows, and bit for bit against a repeat of the
-    same call (a counter not cleared would leave outputs unwritten or half-summed)
-    and against the 16-row call's rows (the split depends on the shape only)."""
+    same call and against the 16-row call's rows (the split depends on the shape
+    only).  The calls run back to back on one weight, so each starts from the count
+    its predecessors left (0, splits, 2 splits, ...): a wrong choice of last
+    workgroup would leave outputs unwritten (NaN) or half-summed."""
     blocks = (synth.kquant_blocks(qtype, N, K, seed=0xB700 + N) if qtype in (12, 14)
               else synth.weight_blocks(qtype, N, K, seed=0xB700 + N))
     x16 = synth.normal(0xB701 + N, (16, K), 1.0)
@@ -116,9 +118,9 @@ def test_batch_k_split(qmm, orc, qtype, N, K):
 def test_k_split_graph_replays_match_eager(qmm):
     """K-split batched GEMVs captured in a HIP graph, as a serving loop replays a
     decode step.  Every replay must equal the eager result bit for bit. Eager calls
-    on the same weights run between the replays: each call must leave the split
-    counters at zero for the next, captured or not. No memset node is involved; the
-    counters are cleared by the kernels themselves."""
+    on the same weights run between the replays: each call, captured or not, must
+    leave the split counters at a multiple of the split count for the next. No
+    memset node is involved; the counters are only ever incremented by the kernels."""
     from openmini_qmm import hip_runtime as hipr
     cases = [(Q4_0, 1024, 8192, 16), (Q8_0, 4096, 8192, 8), (Q4_0, 4096, 4096, 4)]
     st = qmm.Stream()
