@@ -18,10 +18,12 @@
  *
  * Reference paths are relative to openmini-server/ of skin1987/OpenMini-V1.
  *
- * Threading: a weight handle is immutable after upload and may be shared by
- * threads; each call runs on the stream it is given (NULL = the device's null
- * stream).  Device pointers (d_*) must stay valid until the stream reaches the
- * call.  Host-pointer calls (no d_ prefix) are synchronous.
+ * Threading: a weight's quantized data is immutable after upload and its handle may
+ * be shared by threads; each call runs on the stream it is given (NULL = the
+ * device's null stream).  A weight that splits K in batched calls also carries
+ * mutable scratch (see openmini_qmm_gemv) that orders such calls on one weight.
+ * Device pointers (d_*) must stay valid until the stream reaches the call.
+ * Host-pointer calls (no d_ prefix) are synchronous and safe from any thread.
  */
 #pragma once
 
@@ -160,13 +162,14 @@ int openmini_qmm_weight_info(const openmini_qweight_t* weight,
  * weight type.
  * A weight of at most 8192 rows and K >= 4000 splits K of a batched call over two or
  * four workgroups per row tile; their partial sums and arrival counters live in a
- * workspace after the weight's chunks (counted in device_bytes: 128 or 256 B per
- * row plus one word per tile group).  Batched calls (4+ rows, here and in
+ * mutable workspace after the weight's chunks (counted in device_bytes: 128 or 256 B
+ * per row plus one word per tile group).  Batched calls (4+ rows, here and in
  * openmini_qmm_gemv_multi) on one such weight must therefore not overlap in time
- * (two streams with no ordering between them): they would share the workspace.
- * openmini_qmm_linear_host / _noalloc serialise their own such calls per weight.
- * Calls of up to 3 rows, the SwiGLU pair and calls on different weights share no
- * state.
+ * (two streams with no ordering between them): they would share the workspace and
+ * could return wrong sums.  The counters only grow, by the split count per call, so
+ * calls after an overlap are correct again.  openmini_qmm_linear_host / _noalloc
+ * serialise their own such calls per weight.  Calls of up to 3 rows, the SwiGLU
+ * pair and calls on different weights share no state.
  * d_x must be 16-byte aligned. */
 int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float* d_y,
                       int64_t batch, void* stream);
@@ -214,8 +217,10 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
  * the process ends (x first, y from the next 256-byte boundary): m * (K + N) * 4
  * bytes must fit in 16 MiB - 256, else INVALID_PARAM naming the row limit.  Same
  * kernels and results as openmini_qmm_linear_host, synchronous on the null stream.
- * All calls on one device share the array, so calls that overlap on one device race;
- * nothing in it needs clearing (x and y are written whole by every call). */
+ * All calls on one device share the array: the library holds a per-device lock from
+ * the copy in to the copy out, so calls from several threads are safe and run one at
+ * a time per device.  Nothing in the array needs clearing (x and y are written whole
+ * by every call). */
 int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const float* x, float* y,
                                      int64_t m);
 

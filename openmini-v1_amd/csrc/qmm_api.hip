@@ -97,14 +97,15 @@ int check_elements(size_t n) {
 }
 
 // Device probing is done once per device; the result is cached.
+constexpr int kMaxDevices = 64;  // device ordinals the per-device tables cover
 std::mutex g_dev_mu;
-int g_dev_state[64];  // 0 unknown, 1 gfx950, -1 unusable
+int g_dev_state[kMaxDevices];  // 0 unknown, 1 gfx950, -1 unusable
 
 int ensure_device(int* out_dev) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    if (dev < 0 || dev >= 64) return fail(OPENMINI_QMM_ERR_HIP, "device ordinal %d out of range", dev);
+    if (dev < 0 || dev >= kMaxDevices) return fail(OPENMINI_QMM_ERR_HIP, "device ordinal %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_dev_mu);
     if (g_dev_state[dev] == 0) {
         hipDeviceProp_t p;
@@ -207,10 +208,16 @@ constexpr size_t kScratchBytes = (size_t)16 << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 std::mutex g_scratch_mu;
-uint8_t* g_scratch_ptr[64];  // per device ordinal; nullptr until resolved
+uint8_t* g_scratch_ptr[kMaxDevices];  // per device ordinal; nullptr until resolved
+// One staging user per device at a time: openmini_qmm_linear_host_noalloc holds its
+// device's lock across the copy in, the launch and the copy out (the call is
+// synchronous, so the lock costs nothing beyond the serialisation the shared array
+// needs anyway).
+std::mutex g_staging_mu[kMaxDevices];
 
 // The current device's address of `scratch` (dev = the current device).
 int scratch_on_device(int dev, uint8_t** out) {
+    if (dev < 0 || dev >= kMaxDevices) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "device ordinal %d out of range", dev);
     hipError_t e = hipSuccess;
     {
         std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -550,6 +557,7 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
     uint8_t* base = nullptr;
     rc = scratch_on_device(w.device, &base);
     if (rc != OPENMINI_QMM_OK) return rc;
+    std::lock_guard<std::mutex> staging(g_staging_mu[w.device]);
     std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
     if (w.split_s > 1 && qmm::use_batch_kernel(w, m)) lk.lock();
     const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);

@@ -14,7 +14,9 @@ use crate::model::inference::error::{InferenceError, InferenceResult};
 use crate::model::inference::gemm_engine::GemmBackendType;
 use crate::model::inference::gguf::GgufTensorType;
 
-/// A GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor W[n, k] repacked in HBM; immutable after upload.
+/// A GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor W[n, k] repacked in HBM; the quantized data is
+/// immutable after upload (a weight that splits K in batched calls also holds their
+/// scratch, which the library orders for the host-pointer calls this engine makes).
 pub struct HipQuantWeight {
     pub(crate) raw: *mut ffi::QWeight,
     pub n: usize,

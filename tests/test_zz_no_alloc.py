@@ -1,7 +1,7 @@
 """openmini_qmm_linear_host_noalloc (the entry point that allocates nothing) against
 openmini_qmm_linear_host, through the C-ABI.
 
-Both run the same GEMV kernels on the same inputs, so the outputs must be bitwise
+Both run the same kernels on the same inputs, so the outputs must be bitwise
 identical; each is also checked against the fp64 oracle (model.rs:1050-1064, 1e-3).
 Two calls in a row share the library's staging array: the second, smaller call must
 not see the first call's data.  A call past the staging size is rejected."""
@@ -62,3 +62,69 @@ def test_noalloc_rejects_past_staging(qmm):
     xs = synth.normal(0xA31, (rows_max, K), 1.0)
     ys, ys_ref = _both(qmm, w, xs)
     assert np.array_equal(ys.view(np.uint32), ys_ref.view(np.uint32))
+
+
+def test_noalloc_concurrent_threads(qmm):
+    """Four host threads call the entry point at once, each on its own weight (both
+    kernels, a K-split weight among them).  The library serialises the shared staging
+    array per device, so every result must equal the single-threaded linear_host
+    result for the same inputs, bit for bit."""
+    import threading
+    L = _native.lib()
+    cases = [(Q4_0, 4096, 4096, 9, 0xA40), (Q8_0, 1000, 2080, 3, 0xA41), (Q4_0, 2048, 8192, 16, 0xA42),
+             (Q8_0, 3000, 1024, 1, 0xA43)]
+    work = []
+    for qtype, N, K, m, seed in cases:
+        w = qmm.QuantizedWeight(qtype, synth.weight_blocks(qtype, N, K, seed=seed), N, K)
+        xs = [synth.normal(seed + 1 + r, (m, K), 1.0) for r in range(6)]
+        refs = []
+        for x in xs:
+            y = np.full((m, N), np.nan, np.float32)
+            _native.check(L.openmini_qmm_linear_host(w.handle, _ptr(x), _ptr(y), m))
+            refs.append(y)
+        work.append((w, xs, refs))
+    errors = []
+
+    def run(i):
+        w, xs, refs = work[i]
+        try:
+            for r, (x, ref) in enumerate(zip(xs, refs)):
+                y = np.full_like(ref, np.nan)
+                rc = L.openmini_qmm_linear_host_noalloc(w.handle, _ptr(x), _ptr(y), x.shape[0])
+                if rc != 0:
+                    errors.append((i, r, rc, L.openmini_qmm_last_error()))
+                elif not np.array_equal(y.view(np.uint32), ref.view(np.uint32)):
+                    errors.append((i, r, "differs from linear_host"))
+        except Exception as e:  # reported below, on the main thread
+            errors.append((i, repr(e)))
+
+    print("noalloc: 4 threads x 6 calls", flush=True)
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(len(work))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
+def test_noalloc_leaves_device_memory_unchanged(qmm):
+    """After a warm-up call, further calls leave the device's free memory where it
+    was (hipMemGetInfo): the staging array is static, nothing is allocated or kept."""
+    import ctypes as C
+    from openmini_qmm import hip_runtime as hipr
+    H = hipr.hip()
+    H.hipMemGetInfo.restype = C.c_int
+    H.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+    L = _native.lib()
+    N, K, m = 4096, 4096, 12
+    w = qmm.QuantizedWeight(Q4_0, synth.weight_blocks(Q4_0, N, K, seed=0xA50), N, K)
+    x = synth.normal(0xA51, (m, K), 1.0)
+    y = np.empty((m, N), np.float32)
+    _native.check(L.openmini_qmm_linear_host_noalloc(w.handle, _ptr(x), _ptr(y), m))
+    free0, total = C.c_size_t(), C.c_size_t()
+    assert H.hipMemGetInfo(C.byref(free0), C.byref(total)) == 0
+    for _ in range(5):
+        _native.check(L.openmini_qmm_linear_host_noalloc(w.handle, _ptr(x), _ptr(y), m))
+    free1 = C.c_size_t()
+    assert H.hipMemGetInfo(C.byref(free1), C.byref(total)) == 0
+    assert free1.value == free0.value, (free0.value, free1.value)
