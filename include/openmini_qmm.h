@@ -181,6 +181,20 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
 int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
                            int64_t m, void* stream);
 
+/* Prefill GEMM on fp32 activations, linear_gemm's input type (model.rs:1060-1064):
+ * y[m, N] = x[m, K] . W^T, fp32 in and out.  A first kernel writes each row of x,
+ * scaled by a power of two per row, as fp16 hi + lo parts (x carried to within
+ * 2^-22 of each element; elements more than 2^17 below their row's largest keep an
+ * absolute error below 2^-39 of it) into d_work; the GEMM then runs two chained fp16
+ * MFMAs per block on exact fp16 codes and rescales per block in fp32.  A row holding
+ * inf or NaN gives NaN outputs in that row.  d_work: at least
+ * openmini_qmm_gemm_f32_workspace_bytes(m, K) bytes, 256-byte aligned, not shared
+ * with another call in flight; d_x 16-byte aligned.  Every weight type of
+ * openmini_qmm_gemm_bf16. */
+size_t openmini_qmm_gemm_f32_workspace_bytes(int64_t m, int64_t k_cols);
+int openmini_qmm_gemm_f32(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t m,
+                          void* d_work, size_t work_bytes, void* stream);
+
 /* ---- projections of one layer (src/model/inference/model.rs) ----------------------- */
 
 /* Weights that share the input: d_ys[i][batch, N_i] = x[batch, K] . W_i^T for
@@ -205,8 +219,17 @@ int openmini_qmm_ffn_gate_up(const openmini_qweight_t* gate, const openmini_qwei
 int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini_qweight_t* up,
                                   const uint16_t* d_x, float* d_h, int64_t m, void* stream);
 
+/* The same for prefill with fp32 activations: x is split once into d_work (as in
+ * openmini_qmm_gemm_f32, same size and alignment rules), then the gate GEMM and the up
+ * GEMM with the silu(gate) * up epilogue. */
+int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_qweight_t* up,
+                                 const float* d_x, float* d_h, int64_t m, void* d_work, size_t work_bytes,
+                                 void* stream);
+
 /* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
- * fp32 in/out, synchronous.  Uses the GEMV kernels (exact fp32 activations). */
+ * fp32 in/out, synchronous.  Below 128 rows the decode GEMVs, from 128 rows on the
+ * fp32 prefill GEMM (openmini_qmm_gemm_f32); x, y and the GEMM's workspace are
+ * allocated per call. */
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,
                              int64_t m);
 
@@ -214,9 +237,11 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  x and y are staged through a
  * fixed 16 MiB device array that the library holds on every device it runs on until
- * the process ends (x first, y from the next 256-byte boundary): m * (K + N) * 4
- * bytes must fit in 16 MiB - 256, else INVALID_PARAM naming the row limit.  Same
- * kernels and results as openmini_qmm_linear_host, synchronous on the null stream.
+ * the process ends: x, then (from 128 rows on) the fp32 GEMM's workspace, then y, each
+ * from a 256-byte boundary.  About m * (K + N) * 4 bytes below 128 rows and
+ * m * (2 K + N + 1) * 4 from 128 rows on must fit in 16 MiB, else INVALID_PARAM naming
+ * the row limit.  Same kernels and results as openmini_qmm_linear_host, synchronous
+ * on the null stream.
  * All calls on one device share the array: the library holds a per-device lock from
  * the copy in to the copy out, so calls from several threads are safe and run one at
  * a time per device.  Nothing in the array needs clearing (x and y are written whole

@@ -439,6 +439,39 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     return ok();
 }
 
+size_t openmini_qmm_gemm_f32_workspace_bytes(int64_t m, int64_t k_cols) {
+    if (m <= 0 || k_cols <= 0 || m > INT32_MAX || k_cols > INT32_MAX / 2) return 0;
+    return qmm::gemm_f32_workspace_bytes(m, k_cols);
+}
+
+namespace {
+// Shared checks of the fp32-activation GEMM entry points.
+int check_f32_gemm_args(const qmm::Weight& w, const float* d_x, const void* d_out, int64_t m, const void* d_work,
+                        size_t work_bytes) {
+    if (!d_x || !d_out || !d_work) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x, output or workspace");
+    if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
+    if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    if (((uintptr_t)d_work & 255u) != 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "workspace must be 256-byte aligned");
+    const size_t need = qmm::gemm_f32_workspace_bytes(m, w.k);
+    if (work_bytes < need)
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "workspace of %zu bytes, %zu needed for m=%lld, K=%lld", work_bytes,
+                    need, (long long)m, (long long)w.k);
+    return OPENMINI_QMM_OK;
+}
+}  // namespace
+
+int openmini_qmm_gemm_f32(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t m, void* d_work,
+                          size_t work_bytes, void* stream) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    rc = check_f32_gemm_args(weight->w, d_x, d_y, m, d_work, work_bytes);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    hipError_t e = qmm::split_rows(d_x, m, weight->w.k, d_work, as_stream(stream));
+    if (e == hipSuccess) e = qmm::launch_gemm_split(weight->w, d_work, m, d_y, as_stream(stream), false);
+    if (e != hipSuccess) return hip_fail(e, "gemm_f32 launch");
+    return ok();
+}
+
 int openmini_qmm_gemv_multi(const openmini_qweight_t* const* weights, int count, const float* d_x,
                             float* const* d_ys, int64_t batch, void* stream) {
     if (!weights || !d_ys) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null weights or outputs");
@@ -515,6 +548,32 @@ int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini
     return ok();
 }
 
+int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_qweight_t* up, const float* d_x,
+                                 float* d_h, int64_t m, void* d_work, size_t work_bytes, void* stream) {
+    int rc = check_pair(gate, up);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    rc = check_f32_gemm_args(gate->w, d_x, d_h, m, d_work, work_bytes);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    // one split of x for both weights; the up GEMM finishes silu(gate) * up
+    hipError_t e = qmm::split_rows(d_x, m, gate->w.k, d_work, as_stream(stream));
+    if (e == hipSuccess) e = qmm::launch_gemm_split(gate->w, d_work, m, d_h, as_stream(stream), false);
+    if (e == hipSuccess) e = qmm::launch_gemm_split(up->w, d_work, m, d_h, as_stream(stream), true);
+    if (e != hipSuccess) return hip_fail(e, "ffn_gate_up_f32 launch");
+    return ok();
+}
+
+namespace {
+// linear(x, W) on device buffers: the decode GEMVs below qmm::kGemmMinRows rows, else the
+// fp32-activation prefill GEMM (its workspace at d_work).
+hipError_t linear_rows(const qmm::Weight& w, const float* dx, float* dy, int64_t m, void* d_work) {
+    if (m >= qmm::kGemmMinRows) {
+        hipError_t e = qmm::split_rows(dx, m, w.k, d_work, nullptr);
+        return e == hipSuccess ? qmm::launch_gemm_split(w, d_work, m, dy, nullptr, false) : e;
+    }
+    return qmm::launch_gemv_rows(w, nullptr, dx, dy, m, nullptr);
+}
+}  // namespace
+
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y, int64_t m) {
     int rc = check_weight(weight);
     if (rc != OPENMINI_QMM_OK) return rc;
@@ -522,21 +581,20 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
     if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
     const qmm::Weight& w = weight->w;
     std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
-    if (w.split_s > 1 && qmm::use_batch_kernel(w, m)) lk.lock();
-    const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
-    void *dx = nullptr, *dy = nullptr;
-    hipError_t e = hipMalloc(&dx, xb);
-    if (e == hipSuccess) e = hipMalloc(&dy, yb);
-    if (e != hipSuccess) {
-        (void)hipFree(dx);
-        return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
-    }
-    e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = qmm::launch_gemv_rows(w, nullptr, static_cast<const float*>(dx), static_cast<float*>(dy), m, nullptr);
+    if (w.split_s > 1 && m < qmm::kGemmMinRows && qmm::use_batch_kernel(w, m)) lk.lock();
+    if (m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
+    const size_t xb = round_up((size_t)m * w.k * sizeof(float), 256), yb = (size_t)m * w.n * sizeof(float);
+    const size_t wb = m >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, xb + wb + yb);
+    if (e != hipSuccess) return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
+    float* dx = static_cast<float*>(base);
+    uint8_t* work = static_cast<uint8_t*>(base) + xb;
+    float* dy = reinterpret_cast<float*>(work + wb);
+    e = hipMemcpy(dx, x, (size_t)m * w.k * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = linear_rows(w, dx, dy, m, work);
     if (e == hipSuccess) e = hipMemcpy(y, dy, yb, hipMemcpyDeviceToHost);
-    (void)hipFree(dx);
-    (void)hipFree(dy);
+    (void)hipFree(base);
     if (e != hipSuccess) return hip_fail(e, "linear_host");
     return ok();
 }
@@ -547,24 +605,33 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
     if (!x || !y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
     const qmm::Weight& w = weight->w;
-    const size_t row_bytes = (size_t)(w.k + w.n) * sizeof(float);  // one row of x and of y
-    const size_t limit = kScratchBytes - 256;                        // y starts 256-aligned
-    if ((uint64_t)m > limit / row_bytes)
+    // staging: x, the GEMM's workspace (from kGemmMinRows rows on), y, each 256-aligned
+    auto staged_bytes = [&](int64_t rows) {
+        const size_t wb = rows >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(rows, w.k) : 0;
+        return round_up((size_t)rows * w.k * sizeof(float), 256) + wb + (size_t)rows * w.n * sizeof(float);
+    };
+    if (m > INT32_MAX || staged_bytes(m) > kScratchBytes) {
+        int64_t rows_max = 0;  // the largest accepted m (staged_bytes grows with m)
+        for (int64_t step = (int64_t)1 << 30; step > 0; step >>= 1)
+            if (staged_bytes(rows_max + step) <= kScratchBytes) rows_max += step;
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM,
                     "linear_host_noalloc: m=%lld rows of x[K=%lld] and y[N=%lld] need more than the %zu-byte "
-                    "staging (at most %zu rows for this weight)",
-                    (long long)m, (long long)w.k, (long long)w.n, kScratchBytes, limit / row_bytes);
+                    "staging (at most %lld rows for this weight)",
+                    (long long)m, (long long)w.k, (long long)w.n, kScratchBytes, (long long)rows_max);
+    }
     uint8_t* base = nullptr;
     rc = scratch_on_device(w.device, &base);
     if (rc != OPENMINI_QMM_OK) return rc;
     std::lock_guard<std::mutex> staging(g_staging_mu[w.device]);
     std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
-    if (w.split_s > 1 && qmm::use_batch_kernel(w, m)) lk.lock();
-    const size_t xb = (size_t)m * w.k * sizeof(float), yb = (size_t)m * w.n * sizeof(float);
+    if (w.split_s > 1 && m < qmm::kGemmMinRows && qmm::use_batch_kernel(w, m)) lk.lock();
+    const size_t xb = round_up((size_t)m * w.k * sizeof(float), 256), yb = (size_t)m * w.n * sizeof(float);
+    const size_t wb = m >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
     float* dx = reinterpret_cast<float*>(base);
-    float* dy = reinterpret_cast<float*>(base + round_up(xb, 256));
-    hipError_t e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = qmm::launch_gemv_rows(w, nullptr, dx, dy, m, nullptr);
+    uint8_t* work = base + xb;
+    float* dy = reinterpret_cast<float*>(work + wb);
+    hipError_t e = hipMemcpy(dx, x, (size_t)m * w.k * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = linear_rows(w, dx, dy, m, work);
     if (e == hipSuccess) e = hipMemcpy(y, dy, yb, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "linear_host_noalloc");
     return ok();

@@ -1,0 +1,51 @@
+// Device helpers shared by the kernels (gfx950).
+#pragma once
+
+#include "qmm_internal.hpp"
+
+namespace qmm {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (gfx9 descriptor): out-of-range loads return zero, offsets are
+// 32-bit with the uniform part in an SGPR.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
+constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+
+// Two code bytes (selector bytes a, b of `u`) -> the fp16 pair (1024 + u_a, 1024 + u_b).
+__device__ __forceinline__ uint32_t magic_pair(uint32_t u, uint32_t sel) {
+    return __builtin_amdgcn_perm(0x64646464u, u, sel);
+}
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
+
+__device__ __forceinline__ uint32_t pk_sub(uint32_t v, _Float16 c) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, v) - f16x2{c, c});
+}
+
+// Q4_0 code word (elements 8 kq + i in the low nibble of byte i, 8 kq + 4 + i in the
+// high nibble; nibble = (q - 8) mod 16) -> 8 fp16 q - 8, elements in order: the 1024 + u
+// pattern (0x64XX is the fp16 1024 + XX, spacing 1) and one packed fp16 subtraction.
+__device__ __forceinline__ f16x8 codes_q4(uint32_t w) {
+    const uint32_t u = w ^ 0x88888888u;  // nibbles q
+    const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+    uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1032.0f),
+                     pk_sub(magic_pair(hi, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1032.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
+// 8 Q8_0 codes (two words, int8) -> 8 fp16 q.
+__device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128
+    uint32_t p[4] = {pk_sub(magic_pair(u0, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u0, kSel23), (_Float16)1152.0f),
+                     pk_sub(magic_pair(u1, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u1, kSel23), (_Float16)1152.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
+}  // namespace qmm

@@ -29,13 +29,10 @@
 //     registers two K steps ahead (three register sets: first-touch weights come
 //     from HBM, whose latency under load exceeds one step) and converts its own B
 //     fragments (its columns are its own, so nothing is converted twice).
-#include "qmm_internal.hpp"
+#include "qmm_device.hpp"
 
 namespace qmm {
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBMMax = 128;  // most x rows per workgroup
 constexpr int kWT = 3;    // weight tiles (16 columns each) per wave
@@ -73,11 +70,6 @@ __device__ __forceinline__ bf16x8 cvt_q8(uint32_t w0, uint32_t w1) {
     uint32_t p[4] = {pack_hi16(f[0], f[1]), pack_hi16(f[2], f[3]), pack_hi16(f[4], f[5]),
                      pack_hi16(f[6], f[7])};
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<uint4*>(p));
-}
-
-// Raw buffer resource (gfx9 descriptor): out-of-range loads return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
 // Chunk geometry the GEMM reads, by weight format (layouts in qmm_internal.hpp).
@@ -138,8 +130,28 @@ __device__ __forceinline__ void split_q6(uint32_t w, uint32_t hm, int kq, float 
     lo = __builtin_bit_cast(bf16x8, *reinterpret_cast<uint4*>(l));
 }
 
-// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
-constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
+// The same q * sc as fp16 hi (rounded toward zero: 11 significant bits) + lo (the
+// remaining at most 2 bits), both exact.
+__device__ __forceinline__ void split_q6_f16(uint32_t w, uint32_t hm, int kq, float sc4, f16x8& hi, f16x8& lo) {
+    const int sh = (kq & 1) * 4;
+    const uint32_t b0 = ((w << 2) & 0x3C3C3C3Cu) | ((hm << (6 - sh)) & 0xC0C0C0C0u);
+    const uint32_t b1 = ((w >> 2) & 0x3C3C3C3Cu) | ((hm << (4 - sh)) & 0xC0C0C0C0u);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i] = (float)(int8_t)((b0 >> (8 * i)) & 0xFFu) * sc4;
+        f[4 + i] = (float)(int8_t)((b1 >> (8 * i)) & 0xFFu) * sc4;
+    }
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const auto hp = __builtin_amdgcn_cvt_pkrtz(f[2 * p], f[2 * p + 1]);
+        h[p] = __builtin_bit_cast(uint32_t, hp);
+        l[p] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f[2 * p] - (float)hp[0], f[2 * p + 1] - (float)hp[1]));
+    }
+    hi = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(h));
+    lo = __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(l));
+}
 
 // Workgroup shape: kBM x rows, kNW column slices x kKS K parts of waves; a K step is
 // kSB blocks.
@@ -161,16 +173,24 @@ struct Shape {
 
 // kGate: y holds the gate projection on entry and each element is replaced by
 // silu(gate) * (x . W^T), silu(v) = v / (1 + exp(-v)) (model.rs:713-735, :1187-1189).
-template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate>
-__global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ chunks, float* __restrict__ y,
-    int m_rows, int n_rows, int n_tiles, int groups, int k) {
+// kX2: x holds split fp32 activations (split_rows_kernel): per 32-element block 32 fp16
+// hi parts, then 32 fp16 lo parts, of x scaled by 2^e per row (x_exp[m] = e); k is
+// then the length of such a row in fp16 elements (twice K).  Each block runs two
+// chained fp16 MFMAs per subtile (hi, then lo, into one fp32 sum) with fp16 codes,
+// then the same rescale; outputs are scaled back by 2^-e.
+// Two waves per SIMD (512 / threads workgroups per CU): the register budget is 256.
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate, bool kX2>
+__global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_kernel(
+    const uint16_t* __restrict__ x, const int* __restrict__ x_exp, const uint8_t* __restrict__ chunks,
+    float* __restrict__ y, int m_rows, int n_rows, int n_tiles, int groups, int k) {
     using S = Shape<kBM, kNW, kKS, kSB>;
     using F = GFmt<kFmt>;
     constexpr int kMI = S::kMI;
     constexpr int kCB = F::kCB;
     constexpr int kChunk = F::kChunk;
-    constexpr int kStepsPerGroup = kTileBlocks / kSB;
+    constexpr int kWB = kX2 ? kSB / 2 : kSB;  // weight blocks per step
+    static_assert(kWB >= 1, "a step holds at least one weight block");
+    constexpr int kStepsPerGroup = kTileBlocks / kWB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLdsB];
 
     const int lane = threadIdx.x & 63;
@@ -216,14 +236,14 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     uint32_t tile_off[kWT];
 #pragma unroll
     for (int j = 0; j < kWT; ++j) tile_off[j] = (uint32_t)min(tile0 + j, n_tiles - 1) * groups * kChunk;
-    auto load_b = [&](BRegs<kFmt, kSB>& B, int u) {
-        const int g = u / kStepsPerGroup, t0 = (u % kStepsPerGroup) * kSB;
+    auto load_b = [&](BRegs<kFmt, kWB>& B, int u) {
+        const int g = u / kStepsPerGroup, t0 = (u % kStepsPerGroup) * kWB;
 #pragma unroll
         for (int j = 0; j < kWT; ++j) {
             const uint32_t soff = tile_off[j] + (uint32_t)g * kChunk;
             if constexpr (F::kKQ) B.d[j] = __builtin_amdgcn_raw_buffer_load_b16(w_rs, F::kDOff + li * 2, soff, 0);
 #pragma unroll
-            for (int tt = 0; tt < kSB; ++tt) {
+            for (int tt = 0; tt < kWB; ++tt) {
                 const uint32_t slot = (uint32_t)((t0 + tt) * kTileRows + li);
                 if constexpr (F::kQ4K)
                     B.s[j][tt] = __builtin_amdgcn_raw_buffer_load_b8(w_rs, F::kScaleOff + slot, soff, 0);
@@ -253,23 +273,25 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
 #pragma unroll
         for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // A fragments of block tt of the step in LDS stage `stage`: rows i * 16 + li,
-    // elements 8 kq .. 8 kq + 7 of the block (swizzled segment).
-    typedef bf16x8 AFrags[kMI];
+    // A fragments of 32-element segment tt of the step in LDS stage `stage`: rows
+    // i * 16 + li, elements 8 kq .. 8 kq + 7 of the segment (swizzled); bf16 x, or the
+    // fp16 hi (tt even) / lo (tt odd) parts of one block of split x.
+    typedef uint4 AFrags[kMI];
     auto read_a = [&](AFrags& a, int stage, int tt) {
         const uint8_t* slab = lds + stage * S::kStageB + kh * S::kSlabB;
 #pragma unroll
         for (int i = 0; i < kMI; ++i) {
             const int r = i * 16 + li;
-            a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
-                                                  slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16)));
+            a[i] = *reinterpret_cast<const uint4*>(slab + r * S::kRowB + (((tt * 4 + kq) ^ (r % S::kSegs)) * 16));
         }
     };
+    auto bf = [](const uint4& v) { return __builtin_bit_cast(bf16x8, v); };
+    auto hf = [](const uint4& v) { return __builtin_bit_cast(f16x8, v); };
     // Q6_K block tt: the scale changes every 16 elements, inside an MFMA's 32, so it is
     // folded into the codes: q * sc (exact integers) as bf16 hi + lo, two chained MFMAs
     // per subtile, then one FMA per output with the row's d.
-    auto compute_q6 = [&](const BRegs<kFmt, kSB>& B, const AFrags& a, int tt) {
-        if constexpr (F::kQ6K) {
+    auto compute_q6 = [&](const BRegs<kFmt, kWB>& B, const AFrags& a, int tt) {
+        if constexpr (F::kQ6K && !kX2) {
             bf16x8 bh[kWT], bl[kWT];
             float d[kWT];
 #pragma unroll
@@ -278,15 +300,15 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
                 d[j] = f16_bits_to_f32((uint16_t)B.d[j]);
             }
             f32x4 pp[2];
-            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bh[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bl[0], pp[0], 0, 0, 0);
+            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[0]), bh[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[0]), bl[0], pp[0], 0, 0, 0);
 #pragma unroll
             for (int q = 0; q < kMI * kWT; ++q) {
                 if (q + 1 < kMI * kWT) {
                     const int i1 = (q + 1) / kWT, j1 = (q + 1) % kWT;
-                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i1], bh[j1], f32x4{0.f, 0.f, 0.f, 0.f},
-                                                                               0, 0, 0);
-                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i1], bl[j1], pp[(q + 1) & 1], 0, 0, 0);
+                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[i1]), bh[j1],
+                                                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[i1]), bl[j1], pp[(q + 1) & 1], 0, 0, 0);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -295,7 +317,7 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
         }
     };
     // Block tt of one step: 8 x 3 MFMAs on A fragments `a` and the weight registers.
-    auto compute = [&](const BRegs<kFmt, kSB>& B, const AFrags& a, int tt) {
+    auto compute = [&](const BRegs<kFmt, kWB>& B, const AFrags& a, int tt) {
         if constexpr (F::kQ6K) {
             compute_q6(B, a, tt);
             return;
@@ -318,15 +340,63 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
         }
         // MFMA q + 1 is issued before the FMAs of q (two result registers)
         f32x4 pp[2];
-        pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[0]), b[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < kMI * kWT; ++q) {
             if (q + 1 < kMI * kWT)
                 pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    a[(q + 1) / kWT], b[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    bf(a[(q + 1) / kWT]), b[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
+        }
+    };
+    // Split x, the step's one block: per subtile the hi and the lo fragments times the
+    // same fp16 codes, chained into one fp32 sum (exact products), then the rescale.
+    // Q6_K: q * scale as fp16 hi + lo codes, four chained MFMAs per subtile.
+    auto compute_x2 = [&](const BRegs<kFmt, kWB>& B, const AFrags& ah, const AFrags& al) {
+        if constexpr (kX2) {
+            constexpr int kCodes = F::kQ6K ? 2 : 1;
+            f16x8 b[kWT][kCodes];
+            float d[kWT];
+#pragma unroll
+            for (int j = 0; j < kWT; ++j) {
+                if constexpr (F::kQ6K) {
+                    split_q6_f16(B.c[j][0][0], B.c[j][0][1], kq, (float)(int8_t)(B.s[j][0] & 0xFFu) * 0.25f, b[j][0],
+                                 b[j][1]);
+                    d[j] = f16_bits_to_f32((uint16_t)B.d[j]);
+                } else if constexpr (F::kQ4K) {  // q - 8 codes; block factor d * scale (exact)
+                    b[j][0] = codes_q4(B.c[j][0][0]);
+                    d[j] = f16_bits_to_f32((uint16_t)B.d[j]) * (float)(B.s[j][0] & 0xFFu);
+                } else if constexpr (F::kNib) {
+                    b[j][0] = codes_q4(B.c[j][0][0]);
+                    d[j] = f16_bits_to_f32((uint16_t)B.s[j][0]);
+                } else {
+                    b[j][0] = codes_q8(B.c[j][0][0], B.c[j][0][1]);
+                    d[j] = f16_bits_to_f32((uint16_t)B.s[j][0]);
+                }
+            }
+            auto block = [&](int q) {
+                const int i = q / kWT, j = q % kWT;
+                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(hf(ah[i]), b[j][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(hf(al[i]), b[j][0], t, 0, 0, 0);
+#pragma unroll
+                for (int c = 1; c < kCodes; ++c) {
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(hf(ah[i]), b[j][c], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(hf(al[i]), b[j][c], t, 0, 0, 0);
+                }
+                return t;
+            };
+            // the MFMAs of subtile q + 1 are issued before the FMAs of q
+            f32x4 pp[2];
+            pp[0] = block(0);
+#pragma unroll
+            for (int q = 0; q < kMI * kWT; ++q) {
+                if (q + 1 < kMI * kWT) pp[(q + 1) & 1] = block(q + 1);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
+            }
         }
     };
 
@@ -338,10 +408,10 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     // unconditional (units past this part's end re-load its last unit, a cache hit)
     // so the count of outstanding loads is the same on every path; the compiler's
     // own waits before the barrier then cover only the x copies.
-    constexpr int kBLoads = kWT * (kSB * F::kLoadsPerBlock + F::kLoadsPerTile);
+    constexpr int kBLoads = kWT * (kWB * F::kLoadsPerBlock + F::kLoadsPerTile);
     static_assert(kBLoads <= 63, "vmcnt counts up to 63");
     const int u_last = max(u1 - 1, 0);
-    auto step = [&](int it, const BRegs<kFmt, kSB>& cur, BRegs<kFmt, kSB>& far) {
+    auto step = [&](int it, const BRegs<kFmt, kWB>& cur, BRegs<kFmt, kWB>& far) {
         const int u = u0 + it;
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
         __syncthreads();
@@ -352,6 +422,20 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
         // copies before the weights) that the vmcnt count above relies on.
         asm volatile("" ::: "memory");
         const bool live = u < u1;  // uniform per wave
+        if constexpr (kX2) {  // one block per step: its hi and lo fragments, then the weights
+            AFrags ah, al;
+            if (live) {
+                read_a(ah, it & 1, 0);
+                read_a(al, it & 1, 1);
+                __builtin_amdgcn_s_setprio(3);
+                compute_x2(cur, ah, al);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            asm volatile("" ::: "memory");
+            load_b(far, min(u + 2, u_last));
+            asm volatile("" ::: "memory");
+            return;
+        }
         AFrags a;
         // A block's MFMAs and rescale run at raised wave priority, so the SIMD's other
         // wave (copies, weight loads, a barrier) yields issue slots to them: Q8_0
@@ -376,7 +460,7 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
             }
     };
 
-    BRegs<kFmt, kSB> b0, b1, b2;
+    BRegs<kFmt, kWB> b0, b1, b2;
     issue_x(min(u0, u_last), 0);
     asm volatile("" ::: "memory");
     load_b(b0, min(u0, u_last));
@@ -418,10 +502,19 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
 #pragma unroll
                 for (int j = 0; j < kWT; ++j) acc[i][j] += part[i][j];
         }
+        // split x: the row scale 2^-e of each of the lane's output rows
+        int rexp[kX2 ? kMI : 1][4];
+        if constexpr (kX2) {
+#pragma unroll
+            for (int i = 0; i < kMI; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rexp[i][r] = -x_exp[min(m0 + i * 16 + kq * 4 + r, m_rows - 1)];
+        }
         // lane holds D[4 kq + r][li] of each 16 x 16 subtile
         auto store = [&](int i, int j, int r) {
             float* yp = y + (size_t)(m0 + i * 16 + kq * 4 + r) * n_rows + (tile0 + j) * kTileRows + li;
             float v = acc[i][j][r];
+            if constexpr (kX2) v = __builtin_amdgcn_ldexpf(v, rexp[i][r]);
             if constexpr (kGate) {
                 const float g = *yp;
                 v = g / (1.0f + expf(-g)) * v;
@@ -447,12 +540,14 @@ __global__ __launch_bounds__(64 * kNW * kKS) void gemm_kernel(
     }
 }
 
-template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate>
-hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
+// x rows of kx 2-byte elements (K for bf16 x, 2 K for split x).
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate, bool kX2>
+hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
+                        hipStream_t s) {
     using S = Shape<kBM, kNW, kKS, kSB>;
     const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL((gemm_kernel<kFmt, kBM, kNW, kKS, kSB, kGate>), grid, dim3(S::kThreads), 0, s, x, w.chunks,
-                       y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)w.k);
+    hipLaunchKernelGGL((gemm_kernel<kFmt, kBM, kNW, kKS, kSB, kGate, kX2>), grid, dim3(S::kThreads), 0, s, x, x_exp,
+                       w.chunks, y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)kx);
     return hipGetLastError();
 }
 
@@ -462,22 +557,78 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, float* y, int64_t m,
 // K halves (tile 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers
 // overlap the other's work).  Measured on MI355X, Q8_0 11008 x 4096: M = 128 29.8 us
 // (128 x 48 tiles with 4 K parts: 35.6 us); M = 256 / 512 / 2048 against 64-row tiles
-// and 4 x 2 (128 x 192) tiles: equal or faster.
-template <int kFmt, bool kGate>
-hipError_t launch_kind(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
-    if (m <= kBMMax) return launch_shape<kFmt, 64, 2, 4, 2, kGate>(w, x, y, m, s);
-    return launch_shape<kFmt, 128, 2, 2, 2, kGate>(w, x, y, m, s);
+// and 4 x 2 (128 x 192) tiles: equal or faster.  Split x uses the same shapes with
+// one block per step (its hi and lo parts fill the step's 64-element slab).
+template <int kFmt, bool kGate, bool kX2>
+hipError_t launch_kind(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
+                       hipStream_t s) {
+    if (m <= kBMMax) return launch_shape<kFmt, 64, 2, 4, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    return launch_shape<kFmt, 128, 2, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
 }
 
-template <bool kGate>
-hipError_t launch_type(const Weight& w, const uint16_t* x, float* y, int64_t m, hipStream_t s) {
+template <bool kGate, bool kX2>
+hipError_t launch_type(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
+                       hipStream_t s) {
     switch (w.type) {
-    case OPENMINI_QMM_Q4_0: return launch_kind<OPENMINI_QMM_Q4_0, kGate>(w, x, y, m, s);
-    case OPENMINI_QMM_Q8_0: return launch_kind<OPENMINI_QMM_Q8_0, kGate>(w, x, y, m, s);
-    case OPENMINI_QMM_Q4_K: return launch_kind<OPENMINI_QMM_Q4_K, kGate>(w, x, y, m, s);
-    case OPENMINI_QMM_Q6_K: return launch_kind<OPENMINI_QMM_Q6_K, kGate>(w, x, y, m, s);
+    case OPENMINI_QMM_Q4_0: return launch_kind<OPENMINI_QMM_Q4_0, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case OPENMINI_QMM_Q8_0: return launch_kind<OPENMINI_QMM_Q8_0, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case OPENMINI_QMM_Q4_K: return launch_kind<OPENMINI_QMM_Q4_K, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case OPENMINI_QMM_Q6_K: return launch_kind<OPENMINI_QMM_Q6_K, kGate, kX2>(w, x, x_exp, y, m, kx, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+// fp32 activations for the fp16 MFMA: row m of x [m, k] is scaled by 2^e, e chosen so
+// the row's largest |x| lands in [2^14, 2^15), and each element x' = x 2^e is split
+// into hi = x' rounded toward zero to fp16 (11 significant bits) and lo = x' - hi
+// (exact in fp32, at most 13 bits, |lo| < 2^-10 |x'|) rounded to nearest fp16: the
+// pair carries x' to within 2^-22 |x'|, and to within 2^-25 absolute (2^-39 of the
+// row maximum) for elements more than 2^17 below it, where lo is an fp16 subnormal.
+// Written per 32-element block as 32 hi then 32 lo (x2 row = 2 k fp16), e in
+// x_exp[m].  A row holding inf or NaN is written as NaN (hi) and 0 (lo) with e = 0,
+// so every output of that row is NaN (the decode GEMVs do the same).  One workgroup
+// per row; x rows 16-byte aligned (k % 32 == 0).
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ x, uint16_t* __restrict__ x2,
+                                                         int* __restrict__ x_exp, int k) {
+    __shared__ uint32_t wave_max[4];
+    const size_t row = blockIdx.x;
+    const float4* xr = reinterpret_cast<const float4*>(x + row * (size_t)k);
+    const int quads = k / 4;
+    uint32_t mx = 0;  // largest |x| as bits (inf / NaN above every finite value)
+    for (int i = (int)threadIdx.x; i < quads; i += 256) {
+        const float4 v = xr[i];
+        mx = max(max(mx, __float_as_uint(v.x) & 0x7FFFFFFFu), __float_as_uint(v.y) & 0x7FFFFFFFu);
+        mx = max(max(mx, __float_as_uint(v.z) & 0x7FFFFFFFu), __float_as_uint(v.w) & 0x7FFFFFFFu);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3]));
+    const bool bad = mx >= 0x7F800000u;
+    // max |x| in [2^(f - 1), 2^f): e = 15 - f puts it in [2^14, 2^15)
+    const int e = (bad || mx == 0) ? 0 : 15 - __builtin_amdgcn_frexp_expf(__uint_as_float(mx));
+    uint16_t* out = x2 + row * (size_t)(2 * k);
+    for (int i = (int)threadIdx.x; i < quads; i += 256) {
+        const float4 v = xr[i];
+        uint2 hi, lo;
+        if (bad) {
+            hi = make_uint2(0x7E007E00u, 0x7E007E00u);  // fp16 NaN
+            lo = make_uint2(0u, 0u);
+        } else {
+            const float a0 = __builtin_amdgcn_ldexpf(v.x, e), a1 = __builtin_amdgcn_ldexpf(v.y, e);
+            const float a2 = __builtin_amdgcn_ldexpf(v.z, e), a3 = __builtin_amdgcn_ldexpf(v.w, e);
+            const auto h01 = __builtin_amdgcn_cvt_pkrtz(a0, a1), h23 = __builtin_amdgcn_cvt_pkrtz(a2, a3);
+            hi = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+            const f16x2 l01 = {(_Float16)(a0 - (float)h01[0]), (_Float16)(a1 - (float)h01[1])};
+            const f16x2 l23 = {(_Float16)(a2 - (float)h23[0]), (_Float16)(a3 - (float)h23[1])};
+            lo = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+        }
+        const int b = i >> 3, e0 = (i & 7) * 4;  // 32-element block, element within it
+        *reinterpret_cast<uint2*>(out + b * 64 + e0) = hi;
+        *reinterpret_cast<uint2*>(out + b * 64 + 32 + e0) = lo;
+    }
+    if (threadIdx.x == 0) x_exp[row] = e;
 }
 
 // Compute-only ceiling of the prefill GEMM (Q4_0 / Q8_0): gemm_kernel's grid and
@@ -579,8 +730,39 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
         const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
         const uint16_t* xs = x + m_off * w.k;
         float* ys = y + m_off * w.n;
-        const hipError_t e =
-            gate_in_y ? launch_type<true>(w, xs, ys, mm, s) : launch_type<false>(w, xs, ys, mm, s);
+        const hipError_t e = gate_in_y ? launch_type<true, false>(w, xs, nullptr, ys, mm, w.k, s)
+                                       : launch_type<false, false>(w, xs, nullptr, ys, mm, w.k, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+size_t gemm_f32_workspace_bytes(int64_t m, int64_t k) {
+    return (((size_t)m * (size_t)k * 4 + 255) & ~(size_t)255) + (size_t)m * 4;
+}
+
+hipError_t split_rows(const float* x, int64_t m, int64_t k, void* work, hipStream_t s) {
+    if (m <= 0 || m > INT32_MAX || k <= 0 || k % kQK != 0 || k > INT32_MAX / 2) return hipErrorInvalidValue;
+    uint16_t* x2 = static_cast<uint16_t*>(work);
+    int* x_exp = reinterpret_cast<int*>(static_cast<uint8_t*>(work) + (gemm_f32_workspace_bytes(m, k) - (size_t)m * 4));
+    hipLaunchKernelGGL(split_rows_kernel, dim3((unsigned)m), dim3(256), 0, s, x, x2, x_exp, (int)k);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_split(const Weight& w, const void* work, int64_t m, float* y, hipStream_t s, bool gate_in_y) {
+    const uint16_t* x2 = static_cast<const uint16_t*>(work);
+    const int* x_exp =
+        reinterpret_cast<const int*>(static_cast<const uint8_t*>(work) + (gemm_f32_workspace_bytes(m, w.k) - (size_t)m * 4));
+    const int64_t kx = 2 * w.k;  // fp16 elements per split row
+    const int64_t rows_per_launch = ((((int64_t)1 << 31) - 1) / (kx * 2)) / kBMMax * kBMMax;
+    if (rows_per_launch <= 0) return hipErrorInvalidValue;
+    for (int64_t m_off = 0; m_off < m; m_off += rows_per_launch) {
+        const int64_t mm = m - m_off < rows_per_launch ? m - m_off : rows_per_launch;
+        const uint16_t* xs = x2 + m_off * kx;
+        const int* es = x_exp + m_off;
+        float* ys = y + m_off * w.n;
+        const hipError_t e = gate_in_y ? launch_type<true, true>(w, xs, es, ys, mm, kx, s)
+                                       : launch_type<false, true>(w, xs, es, ys, mm, kx, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -49,7 +49,7 @@
 // A fragments through LDS) while the chunks are still in flight, and finally runs
 // the MFMAs as the chunks arrive.  The W partial sums of a row meet in LDS and are
 // added in wave order (deterministic).
-#include "qmm_internal.hpp"
+#include "qmm_device.hpp"
 
 namespace qmm {
 namespace {
@@ -107,11 +107,6 @@ __device__ __forceinline__ float digit_sum(const i32x4& D) {
     return fmaf((float)hi, 65536.0f, (float)lo);
 }
 
-// Raw buffer resource (gfx9 descriptor): out-of-range loads return zero, offsets are
-// 32-bit with the uniform part in an SGPR.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
 // The weights of one launch (kernel argument, uniform).
 struct GemvGroup {

@@ -48,46 +48,10 @@
 // tile group (batch_split): each stores its sums in the weight's workspace and counts
 // itself in; the last to arrive adds the splits' sums in split order, so the result
 // does not depend on which one finishes last.
-#include "qmm_internal.hpp"
+#include "qmm_device.hpp"
 
 namespace qmm {
 namespace {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// Two code bytes (selector bytes a, b of `u`) -> the fp16 pair (1024 + u_a, 1024 + u_b).
-__device__ __forceinline__ uint32_t magic_pair(uint32_t u, uint32_t sel) {
-    return __builtin_amdgcn_perm(0x64646464u, u, sel);
-}
-constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
-
-__device__ __forceinline__ uint32_t pk_sub(uint32_t v, _Float16 c) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, v) - f16x2{c, c});
-}
-
-// Q4_0 code word (elements 8 kq + i in the low nibble of byte i, 8 kq + 4 + i in the
-// high nibble; nibble = (q - 8) mod 16) -> 8 fp16 q - 8, elements in order.
-__device__ __forceinline__ f16x8 codes_q4(uint32_t w) {
-    const uint32_t u = w ^ 0x88888888u;  // nibbles q
-    const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
-    uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1032.0f),
-                     pk_sub(magic_pair(hi, kSel01), (_Float16)1032.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1032.0f)};
-    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
-}
-
-// 8 Q8_0 codes (two words, int8) -> 8 fp16 q.
-__device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
-    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128
-    uint32_t p[4] = {pk_sub(magic_pair(u0, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u0, kSel23), (_Float16)1152.0f),
-                     pk_sub(magic_pair(u1, kSel01), (_Float16)1152.0f), pk_sub(magic_pair(u1, kSel23), (_Float16)1152.0f)};
-    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
-}
 
 // x - hi for the fp16 hi in the low (kHalf = 0) or high half of h, exact in fp32: one
 // mixed-precision FMA reading hi's half directly.
@@ -125,8 +89,6 @@ __device__ __forceinline__ float quarter_max(float m) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only.
-constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
 // Register transposes across the four 16-lane rows of a wave (gfx950 row swaps:
 // permlane32_swap exchanges rows 2, 3 of its first operand with rows 0, 1 of its

@@ -68,6 +68,12 @@ constexpr int kQK = 32;
 constexpr int kMaxGemvBatch = 4;  // batch rows per launch of the single-row-tuned GEMV
 constexpr int kBatchRows = 16;    // batch rows per launch of the batched GEMV (its MFMA rows)
 constexpr int kMaxGroup = 4;      // weights sharing one GEMV launch
+// From this many activation rows on, linear() on fp32 activations runs the prefill
+// GEMM (split activations, fp16 MFMA) instead of the decode GEMVs.
+// Measured (MI355X, graph replay): the fp32 GEMM overtakes the batched GEMV (one pass
+// over W per 16 rows) at 64-96 rows on 11008-row weights, at 96-128 on 4096-row and
+// 28672 x 8192 weights; from 128 rows it is ahead or even on every BASELINE shape.
+constexpr int64_t kGemmMinRows = 128;
 
 // IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
@@ -152,7 +158,7 @@ struct Weight {
     size_t device_bytes = 0;
     // Batched-GEMV K split (split_s > 1, see batch_split): after the chunks, in the
     // same allocation, split_s x kBatchRows x (n_tiles * 16) fp32 partial sums and one
-    // arrival counter per workgroup tile group (zero between calls).
+    // arrival counter per workgroup tile group (a multiple of split_s between calls).
     int split_t = 1, split_s = 1;
     float* split_part = nullptr;
     uint32_t* split_cnt = nullptr;
@@ -215,6 +221,12 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
                             bool gate_in_y = false);
 // The GEMM's register-only instruction mix on its grid for an m x n x k Q4_0 / Q8_0
 // problem (compute-only ceiling); sink[0] is written only if a sentinel is hit.
+// Prefill GEMM on fp32 activations (qmm_gemm.hip): split_rows writes x [m, k] as fp16
+// hi / lo parts plus a per-row exponent into `work` (gemm_f32_workspace_bytes(m, k)
+// bytes, 256-byte aligned), launch_gemm_split runs the GEMM on them.
+size_t gemm_f32_workspace_bytes(int64_t m, int64_t k);
+hipError_t split_rows(const float* x, int64_t m, int64_t k, void* work, hipStream_t s);
+hipError_t launch_gemm_split(const Weight& w, const void* work, int64_t m, float* y, hipStream_t s, bool gate_in_y);
 hipError_t launch_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, float* sink, hipStream_t s);
 
 // quant_simd::convert_to_soa_layout: output bytes, and the conversion of `len` device

@@ -86,9 +86,12 @@ SIGNATURES = {
     "openmini_qmm_weight_info": (_i, [_p, ctypes.POINTER(WeightInfo)]),
     "openmini_qmm_gemv": (_i, [_p, _p, _p, _i64, _p]),
     "openmini_qmm_gemm_bf16": (_i, [_p, _p, _p, _i64, _p]),
+    "openmini_qmm_gemm_f32_workspace_bytes": (_sz, [_i64, _i64]),
+    "openmini_qmm_gemm_f32": (_i, [_p, _p, _p, _i64, _p, _sz, _p]),
     "openmini_qmm_gemv_multi": (_i, [ctypes.POINTER(_p), _i, _p, ctypes.POINTER(_p), _i64, _p]),
     "openmini_qmm_ffn_gate_up": (_i, [_p, _p, _p, _p, _i64, _p]),
     "openmini_qmm_ffn_gate_up_bf16": (_i, [_p, _p, _p, _p, _i64, _p]),
+    "openmini_qmm_ffn_gate_up_f32": (_i, [_p, _p, _p, _p, _i64, _p, _sz, _p]),
     "openmini_qmm_linear_host": (_i, [_p, _p, _p, _i64]),
     "openmini_qmm_linear_host_noalloc": (_i, [_p, _p, _p, _i64]),
     "openmini_qmm_dequant_weight": (_i, [_p, _p, _p]),

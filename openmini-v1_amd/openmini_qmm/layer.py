@@ -10,8 +10,10 @@ several linear layers on one input:
     (model.rs:1392-1394), here one launch for the three.  RoPE and the attention
     itself are not part of the quantized linear layer.
 
-The host-array methods are synchronous and mirror the reference's signatures; the
-*_device methods take device buffers and a stream and only enqueue work.
+The host-array methods are synchronous and mirror the reference's signatures; from
+GEMM_MIN_ROWS rows on (prefill) they run the fp32-activation GEMMs, below it the
+decode GEMVs.  The *_device methods take device buffers and a stream and only enqueue
+work.
 """
 from __future__ import annotations
 
@@ -20,7 +22,7 @@ import ctypes
 import numpy as np
 
 from ._native import check, lib
-from .ops import DeviceBuffer, InvalidInput, QuantizedWeight
+from .ops import GEMM_MIN_ROWS, DeviceBuffer, InvalidInput, QuantizedWeight, gemm_f32_workspace
 
 MAX_GROUP = 4  # weights per gemv_multi launch
 
@@ -45,6 +47,14 @@ def ffn_gate_up_bf16(gate: QuantizedWeight, up: QuantizedWeight, d_x: DeviceBuff
                      d_h: DeviceBuffer, m: int, stream=None) -> None:
     """The same with bf16 activations (raw bits) on the prefill GEMM."""
     check(lib().openmini_qmm_ffn_gate_up_bf16(gate.handle, up.handle, d_x.ptr, d_h.ptr, int(m), stream))
+
+
+def ffn_gate_up_f32(gate: QuantizedWeight, up: QuantizedWeight, d_x: DeviceBuffer, d_h: DeviceBuffer,
+                    m: int, d_work: DeviceBuffer, stream=None) -> None:
+    """The same with fp32 activations on the prefill GEMM (x split once into d_work,
+    gemm_f32_workspace(m, K) bytes)."""
+    check(lib().openmini_qmm_ffn_gate_up_f32(gate.handle, up.handle, d_x.ptr, d_h.ptr, int(m), d_work.ptr,
+                                             d_work.nbytes, stream))
 
 
 def _rows(x: np.ndarray, k: int) -> np.ndarray:
@@ -89,7 +99,12 @@ class FFNWeights:
         d_x = DeviceBuffer.from_numpy(x)
         d_h = DeviceBuffer(m * self.intermediate_size * 4)
         d_out = DeviceBuffer(m * self.down_proj.n_rows * 4)
-        self.forward_device(d_x, d_h, d_out, m)
+        if m >= GEMM_MIN_ROWS:
+            work = gemm_f32_workspace(m, max(self.hidden_size, self.intermediate_size))
+            ffn_gate_up_f32(self.gate_proj, self.up_proj, d_x, d_h, m, work)
+            self.down_proj.gemm_f32(d_h, d_out, m, work)
+        else:
+            self.forward_device(d_x, d_h, d_out, m)
         return d_out.download(np.float32, (m, self.down_proj.n_rows))
 
     def hidden(self, x: np.ndarray) -> np.ndarray:
@@ -98,7 +113,10 @@ class FFNWeights:
         m = x.shape[0]
         d_x = DeviceBuffer.from_numpy(x)
         d_h = DeviceBuffer(m * self.intermediate_size * 4)
-        ffn_gate_up(self.gate_proj, self.up_proj, d_x, d_h, m)
+        if m >= GEMM_MIN_ROWS:
+            ffn_gate_up_f32(self.gate_proj, self.up_proj, d_x, d_h, m, gemm_f32_workspace(m, self.hidden_size))
+        else:
+            ffn_gate_up(self.gate_proj, self.up_proj, d_x, d_h, m)
         return d_h.download(np.float32, (m, self.intermediate_size))
 
 
@@ -125,7 +143,12 @@ class AttentionWeights:
         d_x = DeviceBuffer.from_numpy(x)
         ws = (self.q_proj, self.k_proj, self.v_proj)
         outs = [DeviceBuffer(m * w.n_rows * 4) for w in ws]
-        self.project_qkv_device(d_x, *outs, m)
+        if m >= GEMM_MIN_ROWS:
+            work = gemm_f32_workspace(m, self.q_proj.k_cols)
+            for w, o in zip(ws, outs):
+                w.gemm_f32(d_x, o, m, work)
+        else:
+            self.project_qkv_device(d_x, *outs, m)
         return tuple(o.download(np.float32, (m, w.n_rows)) for o, w in zip(outs, ws))
 
     def project_o(self, attn: np.ndarray) -> np.ndarray:
@@ -136,9 +159,12 @@ class AttentionWeights:
         m = attn.shape[0]
         d_a = DeviceBuffer.from_numpy(attn)
         d_o = DeviceBuffer(m * self.o_proj.n_rows * 4)
-        self.o_proj.gemv(d_a, d_o, m)
+        if m >= GEMM_MIN_ROWS:
+            self.o_proj.gemm_f32(d_a, d_o, m)
+        else:
+            self.o_proj.gemv(d_a, d_o, m)
         return d_o.download(np.float32, (m, self.o_proj.n_rows))
 
 
 __all__ = ["AttentionWeights", "FFNWeights", "MAX_GROUP", "ffn_gate_up", "ffn_gate_up_bf16",
-           "gemv_multi"]
+           "ffn_gate_up_f32", "gemv_multi"]

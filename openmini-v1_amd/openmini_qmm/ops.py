@@ -213,6 +213,13 @@ class QuantizedWeight:
     def gemm_bf16(self, d_x: DeviceBuffer, d_y: DeviceBuffer, m: int, stream=None) -> None:
         check(lib().openmini_qmm_gemm_bf16(self.handle, d_x.ptr, d_y.ptr, int(m), stream))
 
+    def gemm_f32(self, d_x: DeviceBuffer, d_y: DeviceBuffer, m: int, d_work: "DeviceBuffer" = None,
+                 stream=None) -> None:
+        """Prefill GEMM on fp32 activations (openmini_qmm_gemm_f32); allocates the
+        workspace when none is given."""
+        work = d_work if d_work is not None else gemm_f32_workspace(int(m), self.k_cols)
+        check(lib().openmini_qmm_gemm_f32(self.handle, d_x.ptr, d_y.ptr, int(m), work.ptr, work.nbytes, stream))
+
     def close(self) -> None:
         if self.handle:
             lib().openmini_qmm_free_weight(self.handle)
@@ -223,6 +230,20 @@ class QuantizedWeight:
             self.close()
         except Exception:
             pass
+
+
+def gemm_f32_workspace(m: int, k_cols: int) -> DeviceBuffer:
+    """A device workspace for openmini_qmm_gemm_f32 / _ffn_gate_up_f32 (256-byte aligned:
+    the device allocator's granularity)."""
+    nbytes = int(lib().openmini_qmm_gemm_f32_workspace_bytes(int(m), int(k_cols)))
+    if nbytes == 0:
+        raise InvalidInput(f"no workspace for m={m}, K={k_cols}")
+    return DeviceBuffer(nbytes)
+
+
+# Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
+# (the library's own threshold for openmini_qmm_linear_host).
+GEMM_MIN_ROWS = 128
 
 
 # ---- quant_simd safe API (validated dequantization) on the GPU ----------------------
@@ -398,7 +419,8 @@ class HipQuantGemmEngine:
     def fused_gemm_silu(self, x: np.ndarray, gate: QuantizedWeight, up: QuantizedWeight,
                         bias=None) -> np.ndarray:
         """FFNWeights::forward's hidden state silu(x . Wg^T) * (x . Wu^T) (+ bias)
-        (model.rs:728-731), gate and up in one launch (openmini_qmm_ffn_gate_up).  The
+        (model.rs:728-731): gate and up in one launch (openmini_qmm_ffn_gate_up), or from
+        GEMM_MIN_ROWS rows on the fp32 prefill GEMMs (openmini_qmm_ffn_gate_up_f32).  The
         ndarray fallback's fused_gemm_silu (gemm_engine.rs:112-130) computes
         gate * silu(up) on untransposed weights instead; that branch is not followed."""
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -406,9 +428,15 @@ class HipQuantGemmEngine:
             raise InvalidInput(f"x {x.shape}, gate [{gate.n_rows}, {gate.k_cols}], up [{up.n_rows}, "
                                f"{up.k_cols}] do not match")
         dx = DeviceBuffer.from_numpy(x)
-        dh = DeviceBuffer(x.shape[0] * gate.n_rows * 4)
-        check(lib().openmini_qmm_ffn_gate_up(gate.handle, up.handle, dx.ptr, dh.ptr, x.shape[0], None))
-        h = dh.download(np.float32, (x.shape[0], gate.n_rows))
+        m = x.shape[0]
+        dh = DeviceBuffer(m * gate.n_rows * 4)
+        if m >= GEMM_MIN_ROWS:  # prefill: the fp32 GEMM pair on one split of x
+            work = gemm_f32_workspace(m, gate.k_cols)
+            check(lib().openmini_qmm_ffn_gate_up_f32(gate.handle, up.handle, dx.ptr, dh.ptr, m, work.ptr,
+                                                      work.nbytes, None))
+        else:
+            check(lib().openmini_qmm_ffn_gate_up(gate.handle, up.handle, dx.ptr, dh.ptr, m, None))
+        h = dh.download(np.float32, (m, gate.n_rows))
         return h + np.asarray(bias, dtype=np.float32) if bias is not None else h
 
 

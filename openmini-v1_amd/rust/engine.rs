@@ -87,6 +87,10 @@ pub trait QuantGemmEngine: Send + Sync {
 
 pub struct HipQuantGemmEngine;
 
+/// Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
+/// (openmini_qmm_linear_host makes the same choice).
+pub const GEMM_MIN_ROWS: usize = 128;
+
 fn gen_err(e: String) -> InferenceError {
     InferenceError::generation(e)
 }
@@ -157,9 +161,18 @@ impl QuantGemmEngine for HipQuantGemmEngine {
             unsafe {
                 ffi::check(ffi::openmini_qmm_memcpy_h2d(dx.0, x.as_ptr().cast(), m * k * 4, std::ptr::null_mut()))
                     .map_err(gen_err)?;
-                ffi::check(ffi::openmini_qmm_ffn_gate_up(gate.raw, up.raw, dx.0.cast(), dh.0.cast(), m as i64,
-                                                         std::ptr::null_mut()))
-                    .map_err(gen_err)?;
+                if m >= GEMM_MIN_ROWS {
+                    // prefill: the fp32 GEMM pair on one split of x
+                    let wb = ffi::openmini_qmm_gemm_f32_workspace_bytes(m as i64, k as i64);
+                    let work = DeviceBuf::new(wb).map_err(gen_err)?;
+                    ffi::check(ffi::openmini_qmm_ffn_gate_up_f32(gate.raw, up.raw, dx.0.cast(), dh.0.cast(), m as i64,
+                                                                 work.0, wb, std::ptr::null_mut()))
+                        .map_err(gen_err)?;
+                } else {
+                    ffi::check(ffi::openmini_qmm_ffn_gate_up(gate.raw, up.raw, dx.0.cast(), dh.0.cast(), m as i64,
+                                                             std::ptr::null_mut()))
+                        .map_err(gen_err)?;
+                }
                 ffi::check(ffi::openmini_qmm_memcpy_d2h(h.as_mut_ptr().cast(), dh.0, m * gate.n * 4,
                                                         std::ptr::null_mut()))
                     .map_err(gen_err)?;

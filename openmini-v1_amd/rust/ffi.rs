@@ -99,9 +99,12 @@ extern "C" {
     pub fn openmini_qmm_weight_info(weight: *const QWeight, info: *mut WeightInfo) -> c_int;
     pub fn openmini_qmm_gemv(weight: *const QWeight, d_x: *const f32, d_y: *mut f32, batch: i64, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_gemm_bf16(weight: *const QWeight, d_x: *const u16, d_y: *mut f32, m: i64, stream: *mut c_void) -> c_int;
+    pub fn openmini_qmm_gemm_f32_workspace_bytes(m: i64, k_cols: i64) -> usize;
+    pub fn openmini_qmm_gemm_f32(weight: *const QWeight, d_x: *const f32, d_y: *mut f32, m: i64, d_work: *mut c_void, work_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_gemv_multi(weights: *const *const QWeight, count: c_int, d_x: *const f32, d_ys: *const *mut f32, batch: i64, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_ffn_gate_up(gate: *const QWeight, up: *const QWeight, d_x: *const f32, d_h: *mut f32, batch: i64, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_ffn_gate_up_bf16(gate: *const QWeight, up: *const QWeight, d_x: *const u16, d_h: *mut f32, m: i64, stream: *mut c_void) -> c_int;
+    pub fn openmini_qmm_ffn_gate_up_f32(gate: *const QWeight, up: *const QWeight, d_x: *const f32, d_h: *mut f32, m: i64, d_work: *mut c_void, work_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_linear_host(weight: *const QWeight, x: *const f32, y: *mut f32, m: i64) -> c_int;
     pub fn openmini_qmm_linear_host_noalloc(weight: *const QWeight, x: *const f32, y: *mut f32, m: i64) -> c_int;
     pub fn openmini_qmm_dequant_weight(weight: *const QWeight, d_out: *mut f32, stream: *mut c_void) -> c_int;

@@ -123,6 +123,27 @@ def test_ffn_forward_llama7b(qmm, orc, qtype):
     assert_parity(out, orc.linear_f64(qtype, bd, H, I, h_ref.astype(np.float32)), TOL, "chain")
 
 
+def test_layer_prefill_rows(qmm, orc):
+    """The host-array layer methods at prefill sizes (from GEMM_MIN_ROWS rows on they run
+    the fp32-activation GEMMs): FFNWeights.forward / hidden and AttentionWeights
+    project_qkv / project_o at 160 rows of a 1024-hidden, 2816-intermediate layer."""
+    H, I, M = 1024, 2816, 160
+    assert M >= qmm.GEMM_MIN_ROWS
+    print(f"layer prefill rows M={M}", flush=True)
+    (wg, bg), (wu, bu), (wd, bd) = _weights(qmm, Q4_0, ((I, H), (I, H), (H, I)), seed=0x9650)
+    ffn = qmm.FFNWeights(wg, wu, wd)
+    x = synth.normal(0x9651, (M, H), 1.0)
+    h = ffn.hidden(x)
+    assert_parity(h, orc.ffn_hidden_f64(Q4_0, bg, bu, I, H, x), TOL, "hidden")
+    out = ffn.forward(x)
+    assert_parity(out, orc.linear_f64(Q4_0, bd, H, I, h), TOL, "down")
+    ws = _weights(qmm, Q8_0, ((H, H), (256, H), (256, H), (H, H)), seed=0x9652)
+    attn = qmm.AttentionWeights(*[w for w, _ in ws])
+    for (w, blocks), y in zip(ws[:3], attn.project_qkv(x)):
+        assert_parity(y, orc.linear_f64(Q8_0, blocks, w.n_rows, H, x), TOL, "qkv")
+    assert_parity(attn.project_o(x), orc.linear_f64(Q8_0, ws[3][1], H, H, x), TOL, "o_proj")
+
+
 def test_ffn_gate_up_rejects_mismatched_pair(qmm):
     (wg, _), (wu, _) = _weights(qmm, Q4_0, ((64, 128), (48, 128)), seed=0x9700)
     dx, dh = qmm.DeviceBuffer(128 * 4), qmm.DeviceBuffer(64 * 4)

@@ -3,8 +3,8 @@ openmini_qmm_linear_host, through the C-ABI.
 
 Both run the same kernels on the same inputs, so the outputs must be bitwise
 identical; each is also checked against the fp64 oracle (model.rs:1050-1064, 1e-3).
-Two calls in a row share the library's staging array: the second, smaller call must
-not see the first call's data.  A call past the staging size is rejected."""
+Calls in a row share the library's staging array: a later, smaller call must not see
+an earlier call's data.  A call past the staging size is rejected.""" 
 import ctypes
 
 import numpy as np
@@ -33,10 +33,10 @@ def _both(qmm, w, x):
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_noalloc_matches_linear_host(qmm, orc, qtype):
-    # first call: 9 rows (batched kernel) of a 4096 x 4096 weight; second call: 3 rows
-    # (single-row kernel) of a smaller 1000 x 2080 weight, with the first call's data
-    # still in the staging array
-    for N, K, m, seed in ((4096, 4096, 9, 0xA10), (1000, 2080, 3, 0xA20)):
+    # first call: 150 rows (fp32 prefill GEMM) of a 1000 x 2080 weight; then 9 rows
+    # (batched kernel) of a 4096 x 4096 weight; then 3 rows (single-row kernel) of the
+    # first weight's shape, each with the previous call's data still in the staging array
+    for N, K, m, seed in ((1000, 2080, 150, 0xA00), (4096, 4096, 9, 0xA10), (1000, 2080, 3, 0xA20)):
         print(f"noalloc type={qtype} N={N} K={K} m={m}", flush=True)
         blocks = synth.weight_blocks(qtype, N, K, seed=seed)
         w = qmm.QuantizedWeight(qtype, blocks, N, K)
@@ -46,17 +46,29 @@ def test_noalloc_matches_linear_host(qmm, orc, qtype):
         assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} K={K} m={m}")
 
 
+def _staged_bytes(qmm, rows, N, K):
+    """The staging the entry point needs for `rows` rows: x, from GEMM_MIN_ROWS rows on
+    the fp32 GEMM's workspace (split x and one exponent per row), then y, each from a
+    256-byte boundary."""
+    def up(v):
+        return (v + 255) // 256 * 256
+    work = up(rows * K * 4) + rows * 4 if rows >= qmm.GEMM_MIN_ROWS else 0
+    return up(rows * K * 4) + work + rows * N * 4
+
+
 def test_noalloc_rejects_past_staging(qmm):
     L = _native.lib()
     N, K = 8192, 8192
     blocks = synth.weight_blocks(Q4_0, N, K, seed=0xA30)
     w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
-    rows_max = ((16 << 20) - 256) // ((N + K) * 4)  # 255 rows of x[8192] and y[8192]
+    rows_max = max(r for r in range(1, 600) if _staged_bytes(qmm, r, N, K) <= 16 << 20)
+    assert rows_max >= qmm.GEMM_MIN_ROWS  # the largest call runs the fp32 GEMM
     m = rows_max + 1
     x = np.zeros((m, K), np.float32)
     y = np.full((m, N), 7.0, np.float32)
     assert L.openmini_qmm_linear_host_noalloc(w.handle, _ptr(x), _ptr(y), m) == _native.ERR_INVALID_PARAM
     assert b"staging" in L.openmini_qmm_last_error()
+    assert f"at most {rows_max} rows".encode() in L.openmini_qmm_last_error()
     assert np.all(y == 7.0)  # nothing written
     # the largest accepted call runs and matches the allocating path
     xs = synth.normal(0xA31, (rows_max, K), 1.0)
