@@ -13,6 +13,7 @@ result, computed on the GPU.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -172,3 +173,40 @@ class QuantizedWeightLoader:
     def load_ffn_weights(self, layer_idx: int) -> dict:
         prefix = f"model.layers.{layer_idx}.ffn"
         return {p: self.load_tensor(f"{prefix}.{p}") for p in ("gate_proj", "up_proj", "down_proj")}
+
+    def has_tensor(self, name: str) -> bool:
+        """quant_loader.rs:297-299."""
+        return name in self.gguf.tensors
+
+    def load_norm_weights(self, name: str) -> np.ndarray:
+        """quant_loader.rs:278-286: a norm vector as f32 (any stored type, dequantized on
+        the GPU bit-identically to the reference's load_tensor)."""
+        if name not in self.gguf.tensors:
+            raise GgufError(_native.ERR_NOT_FOUND, f"Tensor not found: {name}")
+        return self.gguf.get_tensor_data_by_ref(self.gguf.tensors[name])
+
+    def load_layer(self, layer_idx: int) -> "QuantizedLayerWeights":
+        """QuantizedModelLoader::load_layer (quant_loader.rs:439-484): the layer's four
+        attention and three FFN projections, uploaded quantized, and its two norm vectors
+        (model.layers.{i}.input_layernorm, .post_attention_layernorm) as f32.  The
+        reference also loads MLA (attention.mla.*) and MoE (moe.*) tensors when present;
+        those are outside the quantized linear layer built here, so they are reported as
+        present (has_mla / has_moe) and not loaded."""
+        return QuantizedLayerWeights(
+            attention=self.load_attention_weights(layer_idx),
+            ffn=self.load_ffn_weights(layer_idx),
+            input_layernorm=self.load_norm_weights(f"model.layers.{layer_idx}.input_layernorm"),
+            post_attention_layernorm=self.load_norm_weights(f"model.layers.{layer_idx}.post_attention_layernorm"),
+            has_mla=self.has_tensor(f"model.layers.{layer_idx}.attention.mla.q_proj"),
+            has_moe=self.has_tensor(f"model.layers.{layer_idx}.moe.router"))
+
+
+@dataclass
+class QuantizedLayerWeights:
+    """QuantizedLayerWeights (quant_loader.rs:24-44) with the projections as GPU handles."""
+    attention: dict
+    ffn: dict
+    input_layernorm: np.ndarray
+    post_attention_layernorm: np.ndarray
+    has_mla: bool = False
+    has_moe: bool = False

@@ -84,4 +84,34 @@ impl HipGguf {
         }
         Ok(m)
     }
+
+    /// QuantizedWeightLoader::has_tensor (quant_loader.rs:297-299).
+    pub fn has_tensor(&self, name: &str) -> bool {
+        self.tensor_info(name).is_ok()
+    }
+
+    /// QuantizedModelLoader::load_layer (quant_loader.rs:439-484): the seven projections
+    /// uploaded quantized and the two norm vectors as f32 (load_norm_weights,
+    /// quant_loader.rs:278-286).  MLA / MoE tensors, which the reference also loads when
+    /// present, are outside the quantized linear layer: reported, not loaded.
+    pub fn load_layer(&self, layer: usize) -> Result<HipLayerWeights, String> {
+        Ok(HipLayerWeights {
+            attention: self.load_attention_weights(layer)?,
+            ffn: self.load_ffn_weights(layer)?,
+            input_layernorm: self.tensor_f32(&format!("model.layers.{layer}.input_layernorm"))?,
+            post_attention_layernorm: self.tensor_f32(&format!("model.layers.{layer}.post_attention_layernorm"))?,
+            has_mla: self.has_tensor(&format!("model.layers.{layer}.attention.mla.q_proj")),
+            has_moe: self.has_tensor(&format!("model.layers.{layer}.moe.router")),
+        })
+    }
+}
+
+/// QuantizedLayerWeights (quant_loader.rs:24-44) with the projections on the GPU.
+pub struct HipLayerWeights {
+    pub attention: HashMap<&'static str, HipQuantWeight>,
+    pub ffn: HashMap<&'static str, HipQuantWeight>,
+    pub input_layernorm: Vec<f32>,
+    pub post_attention_layernorm: Vec<f32>,
+    pub has_mla: bool,
+    pub has_moe: bool,
 }

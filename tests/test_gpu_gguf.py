@@ -111,3 +111,52 @@ def test_tensor_by_ref_f32_f16_alignment(qmm, tmp_path, ttype, shift, ok):
         name = "F32" if ttype == 0 else "F16"
         with pytest.raises(G.GgufError, match=f"{name} data is not properly aligned"):
             g.get_tensor_data_by_ref(g.tensors["t"])
+
+
+@pytest.mark.parametrize("dialect", ["reference", "standard"])
+def test_load_layer(qmm, orc, tmp_path, dialect):
+    """QuantizedModelLoader::load_layer (quant_loader.rs:439-484) on a one-layer file:
+    the seven projections by the reference's names come back as GPU weights that equal
+    direct uploads of the same blocks (dequantized bit for bit, and a GEMV against the
+    oracle), the two norm vectors as f32 bit-identical to the reference's
+    dequantization (one stored F32, one F16); MLA / MoE tensors are reported, not
+    loaded; a missing norm is "Tensor not found"."""
+    H, I = 256, 704
+    rng = np.random.default_rng(21)
+    shapes = {"attention.q_proj": (H, H), "attention.k_proj": (64, H), "attention.v_proj": (64, H),
+              "attention.o_proj": (H, H), "ffn.gate_proj": (I, H), "ffn.up_proj": (I, H),
+              "ffn.down_proj": (H, I)}
+    qtypes = {name: (Q4_0 if i % 2 == 0 else Q8_0) for i, name in enumerate(shapes)}
+    blocks = {name: synth.weight_blocks(qtypes[name], n, k, seed=0x1A00 + i)
+              for i, (name, (n, k)) in enumerate(shapes.items())}
+    ln_in = rng.standard_normal(H).astype(np.float32)
+    ln_post = rng.standard_normal(H).astype(np.float16)
+    tensors = [(f"model.layers.0.{name}", [k, n], qtypes[name], blocks[name].tobytes())
+               for name, (n, k) in shapes.items()]
+    tensors += [("model.layers.0.input_layernorm", [H], 0, ln_in.tobytes()),
+                ("model.layers.0.post_attention_layernorm", [H], 1, ln_post.tobytes()),
+                ("model.layers.0.moe.router", [H], 0, ln_in.tobytes())]
+    path = tmp_path / "one_layer.gguf"
+    path.write_bytes(fx.build([("general.architecture", fx.STRING, "llama")], tensors, dialect))
+    print(f"load_layer dialect={dialect}", flush=True)
+    loader = G.QuantizedWeightLoader.open(str(path))
+    layer = loader.load_layer(0)
+    assert sorted(layer.attention) == ["k_proj", "o_proj", "q_proj", "v_proj"]
+    assert sorted(layer.ffn) == ["down_proj", "gate_proj", "up_proj"]
+    x = synth.normal(0x1A10, (2, I), 1.0)
+    for group, part in (("attention", layer.attention), ("ffn", layer.ffn)):
+        for p, w in part.items():
+            name = f"{group}.{p}"
+            n, k = shapes[name]
+            assert (w.n_rows, w.k_cols, int(w.tensor_type)) == (n, k, qtypes[name])
+            assert np.array_equal(bits(w.dequantize()),
+                                  bits(orc.dequantize(qtypes[name], blocks[name], n * k).reshape(n, k)))
+            dx, dy = qmm.DeviceBuffer.from_numpy(np.ascontiguousarray(x[:, :k])), qmm.DeviceBuffer(2 * n * 4)
+            w.gemv(dx, dy, 2)
+            ref = orc.linear_f64(qtypes[name], blocks[name], n, k, x[:, :k])
+            assert np.max(np.abs(dy.download(np.float32, (2, n)) - ref)) <= 1e-3 * np.max(np.abs(ref))
+    assert np.array_equal(bits(layer.input_layernorm), bits(ln_in))
+    assert np.array_equal(bits(layer.post_attention_layernorm), bits(ln_post.astype(np.float32)))
+    assert layer.has_moe and not layer.has_mla
+    with pytest.raises(G.GgufError, match="Tensor not found"):
+        loader.load_layer(1)
