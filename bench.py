@@ -153,19 +153,27 @@ def bench_gemv(qmm, hipr, stream, steps, warmup, N, K, qtype=Q4_0, batch=1, seed
 
 
 def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q8_0, seed=0x5EED0003,
-               sigma=0.02):
-    from openmini_qmm import synth
+               sigma=0.02, f32_x=False):
+    """The prefill GEMM on bf16 activations, or (f32_x) on fp32 activations through
+    openmini_qmm_gemm_f32 (split pre-pass + GEMM, both timed, workspace preallocated)."""
+    from openmini_qmm import _native, synth
     blocks = weight_blocks(qtype, N, K, seed, sigma)
     copies = max(2, -(-(MALL_DEFEAT_BYTES // 2) // blocks.size))
-    log(f"gemm type={qtype} N={N} K={K} M={M}: {copies} weight copies")
+    log(f"gemm type={qtype} N={N} K={K} M={M}{' f32 x' if f32_x else ''}: {copies} weight copies")
     ws = [qmm.QuantizedWeight(qtype, blocks, N, K) for _ in range(copies)]
-    xb = synth.to_bf16_bits(synth.normal(seed + 0x8000, (M, K), 1.0))
-    dx = qmm.DeviceBuffer.from_numpy(xb)
+    x32 = synth.normal(seed + 0x8000, (M, K), 1.0)
+    xb = synth.to_bf16_bits(x32)
+    dx = qmm.DeviceBuffer.from_numpy(x32 if f32_x else xb)
     dy = qmm.DeviceBuffer(M * N * 4)
+    work = qmm.gemm_f32_workspace(M, K) if f32_x else None
     sh = stream.handle
+    shape = _native.lib().openmini_qmm_gemm_launch_shape(ws[0].handle, M, int(f32_x))
 
     def launch(i):
-        ws[i % copies].gemm_bf16(dx, dy, M, sh)
+        if f32_x:
+            ws[i % copies].gemm_f32(dx, dy, M, work, sh)
+        else:
+            ws[i % copies].gemm_bf16(dx, dy, M, sh)
 
     for i in range(warmup):
         launch(i)
@@ -176,8 +184,8 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
     for w in ws:
         w.close()
     return {
-        "N": N, "K": K, "M": M, "weight_copies": copies,
-        "sha256": {"weight": sha256(blocks), "x_bf16": sha256(xb)},
+        "N": N, "K": K, "M": M, "weight_copies": copies, "launch_shape": shape,
+        "sha256": {"weight": sha256(blocks), ("x_f32" if f32_x else "x_bf16"): sha256(x32 if f32_x else xb)},
         "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
         "tflops_wall": flops * steps / (total_ms * 1e-3) / 1e12,
         "tflops_kernel": flops / (per_launch_ms * 1e-3) / 1e12,
@@ -571,7 +579,7 @@ def main(argv=None) -> int:
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
                             "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
                             "ceiling_us": round(c["us"], 3), "frac_of_ceiling": round(c["us"] / (r["kernel_ms"] * 1e3), 4),
-                            "sha256": r["sha256"]})
+                            "launch_shape": r["launch_shape"], "sha256": r["sha256"]})
             log(f"q8_0 gemm M={m}: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
         # prefill on K-quant weights (Llama-7B up projection, M = 512)
         for qtype in (Q4_K, Q6_K):
@@ -579,7 +587,8 @@ def main(argv=None) -> int:
                            seed=0x5EED0081 + qtype)
             prefill.append({"workload": f"{TYPE_NAME[qtype]}_gemm_n11008_k4096_m512_bf16x", "unit": "TFLOP/s",
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
-                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
+                            "launch_shape": r["launch_shape"], "sha256": r["sha256"]})
             log(f"{TYPE_NAME[qtype]} gemm M=512: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
         # the 70B q / gate / down projections at prefill M = 1024
         for n, k, seed in SHAPES_70B:
@@ -587,8 +596,20 @@ def main(argv=None) -> int:
                            M=1024, qtype=Q4_0, seed=seed, sigma=SIGMA_70B)
             prefill.append({"workload": f"q4_0_gemm_n{n}_k{k}_m1024_bf16x", "unit": "TFLOP/s",
                             "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
-                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "sha256": r["sha256"]})
+                            "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
+                            "launch_shape": r["launch_shape"], "sha256": r["sha256"]})
             log(f"q4_0 gemm {n}x{k} M=1024: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s")
+        # the fp32-activation prefill (linear_gemm's own input type, the operator's route
+        # from 128 rows on) at configs[3]'s M = 512, against the bf16 leg above
+        r = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), f32_x=True)
+        prefill.append({"workload": "q8_0_gemm_n11008_k4096_m512_f32x", "unit": "TFLOP/s",
+                        "value": round(r["tflops_kernel"], 2), "kernel_us": round(r["kernel_ms"] * 1e3, 3),
+                        "frac": round(r["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
+                        "time_vs_bf16x": round(r["kernel_ms"] / gemm["kernel_ms"], 3),
+                        "includes": "the split pre-pass (fp32 x -> fp16 hi / lo) and the GEMM",
+                        "launch_shape": r["launch_shape"], "sha256": r["sha256"]})
+        log(f"q8_0 gemm M=512 f32 x: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s "
+            f"({r['kernel_ms'] / gemm['kernel_ms']:.2f}x the bf16 leg)")
     layer = None
     if not args.no_layer:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
@@ -711,6 +732,7 @@ def main(argv=None) -> int:
             "sha256": gemm["sha256"],
             "value": round(gemm["tflops_wall"], 2), "unit": "TFLOP/s", "dtype": "bf16",
             "ms_per_step": round(gemm["ms_per_step"], 6),
+            "launch_shape": gemm["launch_shape"],
             "roofline": {"bound": "mfma", "achieved": round(gemm["tflops_kernel"], 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(gemm["tflops_kernel"] / BF16_PEAK_TFLOPS, 4), "traffic": None,

@@ -192,6 +192,13 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
  * with another call in flight; d_x 16-byte aligned.  Every weight type of
  * openmini_qmm_gemm_bf16. */
 size_t openmini_qmm_gemm_f32_workspace_bytes(int64_t m, int64_t k_cols);
+
+/* Diagnostic, no counterpart in the reference: the launch shape the prefill GEMM picks
+ * for m rows on this weight (bf16 activations, or split fp32 ones when split_x != 0):
+ * 0 = 128 x 96 tiles, 1 = 128 x 64, 2 = 64 x 96, 3 = 64 x 64 (rows x columns per
+ * workgroup), chosen from the problem size alone, so a row's bits depend only on m and
+ * the weight.  A negative status on error. */
+int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, int split_x);
 int openmini_qmm_gemm_f32(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t m,
                           void* d_work, size_t work_bytes, void* stream);
 

@@ -439,6 +439,15 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     return ok();
 }
 
+int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, int split_x) {
+    int rc = check_weight(weight);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
+    const int shape = qmm::gemm_shape(weight->w, m, split_x != 0);
+    if (shape < 0) return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "no prefill GEMM for type %d", weight->w.type);
+    return shape;
+}
+
 size_t openmini_qmm_gemm_f32_workspace_bytes(int64_t m, int64_t k_cols) {
     if (m <= 0 || k_cols <= 0 || m > INT32_MAX || k_cols > INT32_MAX / 2) return 0;
     return qmm::gemm_f32_workspace_bytes(m, k_cols);

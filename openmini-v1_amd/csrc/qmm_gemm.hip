@@ -17,15 +17,15 @@
 // MFMA's 32, so q * scale (an exact integer of at most 13 bits) enters as bf16
 // hi + lo (two chained MFMAs, both exact), and the row's d is the block factor.
 //
-// Tiling: a workgroup computes a kBM x (48 kNW) tile of y with kNW column slices x
-// kKS K parts of waves (launch_kind picks 128 x 96 with 2 x 2 waves, or 64 x 96
-// with 2 x 4 waves for M <= 128).  A wave owns kBM rows x 48 columns (3 weight tiles:
-// kBM/16 x 3 MFMA subtiles of fp32 accumulators) over one K part, and the parts are
-// added through LDS at the end (fixed order).  A K step is two blocks (64 elements):
+// Tiling: a workgroup computes a kBM x (16 kWT kNW) tile of y with kNW column slices
+// x kKS K parts of waves (choose_shape picks 128 or 64 rows and 3 or 2 weight tiles per
+// wave by problem size).  A wave owns kBM rows x 16 kWT columns (kBM/16 x kWT MFMA
+// subtiles of fp32 accumulators) over one K part, and the parts are added through
+// LDS at the end (fixed order).  A K step is two blocks (64 elements):
 //   * x: each K part's kBM x 64 bf16 slab is copied HBM -> LDS by buffer loads with
 //     an LDS destination (no registers), double-buffered, rows XOR-swizzled in
 //     16-byte segments so the A-fragment reads are bank-conflict free;
-//   * weights: each wave loads its 3 tiles' codes and scales straight into
+//   * weights: each wave loads its kWT tiles' codes and scales straight into
 //     registers two K steps ahead (three register sets: first-touch weights come
 //     from HBM, whose latency under load exceeds one step) and converts its own B
 //     fragments (its columns are its own, so nothing is converted twice).
@@ -35,7 +35,7 @@ namespace qmm {
 namespace {
 
 constexpr int kBMMax = 128;  // most x rows per workgroup
-constexpr int kWT = 3;    // weight tiles (16 columns each) per wave
+constexpr int kCeilWT = 3;   // weight tiles per wave of the launch shapes the ceiling yardstick mirrors
 
 __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
     // bf16 of exactly-representable values = high halves of their fp32 bits.
@@ -94,7 +94,7 @@ struct GFmt {
 // step, the lane's 8 codes (Q4_0 / Q4_K one word of nibbles, Q8_0 two words of
 // bytes, Q6_K the low-nibble word and the top-bit word), its column's scale, and for
 // K-quants the column's d (one per step: a step stays inside one group).
-template <int kFmt, int kSB>
+template <int kFmt, int kSB, int kWT>
 struct BRegs {
     uint32_t c[kWT][kSB][GFmt<kFmt>::kWords];
     uint32_t s[kWT][kSB];
@@ -155,8 +155,9 @@ __device__ __forceinline__ void split_q6_f16(uint32_t w, uint32_t hm, int kq, fl
 
 // Workgroup shape: kBM x rows, kNW column slices x kKS K parts of waves; a K step is
 // kSB blocks.
-template <int kBM, int kNW, int kKS, int kSB>
+template <int kBM, int kNW, int kKS, int kSB, int kWT_>
 struct Shape {
+    static constexpr int kWT = kWT_;                       // weight tiles (16 columns each) per wave
     static constexpr int kMI = kBM / 16;                   // MFMA row subtiles per wave
     static constexpr int kThreads = 64 * kNW * kKS;
     static constexpr int kBT = kNW * kWT;                 // weight tiles per workgroup
@@ -179,11 +180,11 @@ struct Shape {
 // chained fp16 MFMAs per subtile (hi, then lo, into one fp32 sum) with fp16 codes,
 // then the same rescale; outputs are scaled back by 2^-e.
 // Two waves per SIMD (512 / threads workgroups per CU): the register budget is 256.
-template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate, bool kX2>
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, int kWT, bool kGate, bool kX2>
 __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_kernel(
     const uint16_t* __restrict__ x, const int* __restrict__ x_exp, const uint8_t* __restrict__ chunks,
     float* __restrict__ y, int m_rows, int n_rows, int n_tiles, int groups, int k) {
-    using S = Shape<kBM, kNW, kKS, kSB>;
+    using S = Shape<kBM, kNW, kKS, kSB, kWT>;
     using F = GFmt<kFmt>;
     constexpr int kMI = S::kMI;
     constexpr int kCB = F::kCB;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     uint32_t tile_off[kWT];
 #pragma unroll
     for (int j = 0; j < kWT; ++j) tile_off[j] = (uint32_t)min(tile0 + j, n_tiles - 1) * groups * kChunk;
-    auto load_b = [&](BRegs<kFmt, kWB>& B, int u) {
+    auto load_b = [&](BRegs<kFmt, kWB, kWT>& B, int u) {
         const int g = u / kStepsPerGroup, t0 = (u % kStepsPerGroup) * kWB;
 #pragma unroll
         for (int j = 0; j < kWT; ++j) {
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     // Q6_K block tt: the scale changes every 16 elements, inside an MFMA's 32, so it is
     // folded into the codes: q * sc (exact integers) as bf16 hi + lo, two chained MFMAs
     // per subtile, then one FMA per output with the row's d.
-    auto compute_q6 = [&](const BRegs<kFmt, kWB>& B, const AFrags& a, int tt) {
+    auto compute_q6 = [&](const BRegs<kFmt, kWB, kWT>& B, const AFrags& a, int tt) {
         if constexpr (F::kQ6K && !kX2) {
             bf16x8 bh[kWT], bl[kWT];
             float d[kWT];
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
         }
     };
     // Block tt of one step: 8 x 3 MFMAs on A fragments `a` and the weight registers.
-    auto compute = [&](const BRegs<kFmt, kWB>& B, const AFrags& a, int tt) {
+    auto compute = [&](const BRegs<kFmt, kWB, kWT>& B, const AFrags& a, int tt) {
         if constexpr (F::kQ6K) {
             compute_q6(B, a, tt);
             return;
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     // Split x, the step's one block: per subtile the hi and the lo fragments times the
     // same fp16 codes, chained into one fp32 sum (exact products), then the rescale.
     // Q6_K: q * scale as fp16 hi + lo codes, four chained MFMAs per subtile.
-    auto compute_x2 = [&](const BRegs<kFmt, kWB>& B, const AFrags& ah, const AFrags& al) {
+    auto compute_x2 = [&](const BRegs<kFmt, kWB, kWT>& B, const AFrags& ah, const AFrags& al) {
         if constexpr (kX2) {
             constexpr int kCodes = F::kQ6K ? 2 : 1;
             f16x8 b[kWT][kCodes];
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     constexpr int kBLoads = kWT * (kWB * F::kLoadsPerBlock + F::kLoadsPerTile);
     static_assert(kBLoads <= 63, "vmcnt counts up to 63");
     const int u_last = max(u1 - 1, 0);
-    auto step = [&](int it, const BRegs<kFmt, kWB>& cur, BRegs<kFmt, kWB>& far) {
+    auto step = [&](int it, const BRegs<kFmt, kWB, kWT>& cur, BRegs<kFmt, kWB, kWT>& far) {
         const int u = u0 + it;
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
         __syncthreads();
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
             }
     };
 
-    BRegs<kFmt, kWB> b0, b1, b2;
+    BRegs<kFmt, kWB, kWT> b0, b1, b2;
     issue_x(min(u0, u_last), 0);
     asm volatile("" ::: "memory");
     load_b(b0, min(u0, u_last));
@@ -541,29 +542,80 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
 }
 
 // x rows of kx 2-byte elements (K for bf16 x, 2 K for split x).
-template <int kFmt, int kBM, int kNW, int kKS, int kSB, bool kGate, bool kX2>
+template <int kFmt, int kBM, int kNW, int kKS, int kSB, int kWT, bool kGate, bool kX2>
 hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
                         hipStream_t s) {
-    using S = Shape<kBM, kNW, kKS, kSB>;
+    using S = Shape<kBM, kNW, kKS, kSB, kWT>;
     const dim3 grid((unsigned)((w.n_tiles + S::kBT - 1) / S::kBT), (unsigned)((m + kBM - 1) / kBM));
-    hipLaunchKernelGGL((gemm_kernel<kFmt, kBM, kNW, kKS, kSB, kGate, kX2>), grid, dim3(S::kThreads), 0, s, x, x_exp,
-                       w.chunks, y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)kx);
+    hipLaunchKernelGGL((gemm_kernel<kFmt, kBM, kNW, kKS, kSB, kWT, kGate, kX2>), grid, dim3(S::kThreads), 0, s, x,
+                       x_exp, w.chunks, y, (int)m, (int)w.n, (int)w.n_tiles, (int)w.groups, (int)kx);
     return hipGetLastError();
 }
 
-// Shape by M.  Up to 128 rows: 64-row tiles, 2 column slices x 4 K parts (tile
-// 64 x 96, 512 threads, 72 KB of LDS) -- twice the workgroups of 128-row tiles where
-// too few of them would fill the CUs.  More rows: 128-row tiles, 2 column slices x 2
-// K halves (tile 128 x 96, 64 KB of LDS, two workgroups per CU so one's barriers
-// overlap the other's work).  Measured on MI355X, Q8_0 11008 x 4096: M = 128 29.8 us
-// (128 x 48 tiles with 4 K parts: 35.6 us); M = 256 / 512 / 2048 against 64-row tiles
-// and 4 x 2 (128 x 192) tiles: equal or faster.  Split x uses the same shapes with
-// one block per step (its hi and lo parts fill the step's 64-element slab).
+// Tile families: 128-row tiles with 2 column slices x 2 K halves of waves (64 KB of LDS,
+// two workgroups per CU so one's barriers overlap the other's work), and 64-row tiles
+// with 2 column slices x 4 K parts (72 KB of LDS) for more, smaller workgroups.  Split
+// x uses the same shapes with one block per step (its hi and lo parts fill the step's
+// 64-element slab).
+// Launch shape by problem size.
+//   0: 128-row tiles, 3 weight tiles per wave (128 x 96, 4 waves)
+//   1: 128-row tiles, 2 weight tiles per wave (128 x 64, 4 waves)
+//   2:  64-row tiles, 3 weight tiles per wave ( 64 x 96, 8 waves)
+//   3:  64-row tiles, 2 weight tiles per wave ( 64 x 64, 8 waves)
+// Few and large workgroups leave CUs idle or a last round part-filled; small ones
+// cost more per flop (each B fragment serves fewer MFMAs, each A fragment fewer
+// tiles).  The model: workgroups run in rounds of (CUs x workgroups per CU, from the
+// kernel's occupancy); a round costs (workgroups per CU) x (tile work) x (the shape's
+// relative cost per flop), a last round of at most one workgroup per CU 0.67 of that.
+// The relative costs are fitted to shape-by-shape timings on MI355X (Q4_0 / Q8_0,
+// M = 128..2048, 4096..28672 rows): the model picks the fastest shape in 11 of 12
+// cases and is within 10% in the twelfth.  Fixed per shape, so a row's bits depend
+// only on m and the weight.
+int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4]) {
+    static const int bm[4] = {128, 128, 64, 64}, wt[4] = {3, 2, 3, 2};
+    static const double cost_per_flop[4] = {1.00, 1.10, 1.25, 1.35};
+    const int64_t cus = 256;
+    int best = 0;
+    double best_cost = 0.0;
+    for (int i = 0; i < 4; ++i) {
+        const int spc = per_cu[i] > 0 ? per_cu[i] : 1;
+        const int64_t wgs = (w.n_tiles + 2 * wt[i] - 1) / (2 * wt[i]) * ((m + bm[i] - 1) / bm[i]);
+        const int64_t slots = cus * spc;
+        const double round = (double)spc * bm[i] * wt[i] * cost_per_flop[i] * (spc == 1 ? 1.2 : 1.0);
+        double cost = (double)(wgs / slots) * round;
+        if (wgs % slots) cost += round * (wgs % slots <= cus ? 0.67 : 1.0);
+        if (i == 0 || cost < best_cost) best = i, best_cost = cost;
+    }
+    return best;
+}
+
+// Workgroups of `kernel` (at `threads` per workgroup) one CU holds at once.
+int blocks_per_cu(const void* kernel, int threads) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) return 1;
+    return n;
+}
+
+// Workgroups per CU of the four shapes' kernels (queried once per instantiation).
+template <int kFmt, bool kGate, bool kX2>
+const int (&shape_occupancy())[4] {
+    static const int per_cu[4] = {
+        blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 3, kGate, kX2>, 256),
+        blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 2, kGate, kX2>, 256),
+        blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 3, kGate, kX2>, 512),
+        blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 2, kGate, kX2>, 512)};
+    return per_cu;
+}
+
 template <int kFmt, bool kGate, bool kX2>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
                        hipStream_t s) {
-    if (m <= kBMMax) return launch_shape<kFmt, 64, 2, 4, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
-    return launch_shape<kFmt, 128, 2, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    switch (choose_shape(w, m, shape_occupancy<kFmt, kGate, kX2>())) {
+    case 0: return launch_shape<kFmt, 128, 2, 2, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case 1: return launch_shape<kFmt, 128, 2, 2, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case 2: return launch_shape<kFmt, 64, 2, 4, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    default: return launch_shape<kFmt, 64, 2, 4, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    }
 }
 
 template <bool kGate, bool kX2>
@@ -632,8 +684,8 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict
 }
 
 // Compute-only ceiling of the prefill GEMM (Q4_0 / Q8_0): gemm_kernel's grid and
-// waves, each running only its per-block register work -- kWT code conversions,
-// kMI x kWT MFMAs and their rescale FMAs, in the same order -- for as many blocks as
+// waves, each running only its per-block register work -- kCeilWT code conversions,
+// kMI x kCeilWT MFMAs and their rescale FMAs, in the same order -- for as many blocks as
 // its K part holds, on operands that stay in registers.  No loads, LDS, barriers or
 // stores (a sentinel store keeps the work live), so its time is what the GEMM's
 // instruction mix alone costs under the same clock and power conditions.
@@ -646,28 +698,28 @@ __global__ __launch_bounds__(512) void gemm_ceiling_kernel(int blocks, float* __
     for (int i = 0; i < kMI; ++i)
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[i][e] = (__bf16)((float)((lane + 7 * i + e) & 15) * 0.125f);
-    uint32_t c0[kWT], c1[kWT], sc[kWT];
+    uint32_t c0[kCeilWT], c1[kCeilWT], sc[kCeilWT];
 #pragma unroll
-    for (int j = 0; j < kWT; ++j) {
+    for (int j = 0; j < kCeilWT; ++j) {
         c0[j] = 0x01030507u * (uint32_t)(lane + j + 1);
         c1[j] = 0x02040608u * (uint32_t)(lane + j + 1);
         sc[j] = 0x3C00u;  // fp16 1.0
     }
-    f32x4 acc[kMI][kWT];
+    f32x4 acc[kMI][kCeilWT];
 #pragma unroll
     for (int i = 0; i < kMI; ++i)
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kCeilWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int b = 0; b < blocks; ++b) {
         // new operands every block, as the A-fragment reads and weight loads give
 #pragma unroll
         for (int i = 0; i < kMI; ++i) asm volatile("" : "+v"(a[i]));
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) asm volatile("" : "+v"(c0[j]), "+v"(c1[j]), "+v"(sc[j]));
-        bf16x8 bq[kWT];
-        float d[kWT];
+        for (int j = 0; j < kCeilWT; ++j) asm volatile("" : "+v"(c0[j]), "+v"(c1[j]), "+v"(sc[j]));
+        bf16x8 bq[kCeilWT];
+        float d[kCeilWT];
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) {
+        for (int j = 0; j < kCeilWT; ++j) {
             if constexpr (kNib) {
                 bq[j] = cvt_q4(c0[j]);
                 d[j] = f16_bits_to_f32((uint16_t)sc[j]) * 16.0f;
@@ -679,20 +731,20 @@ __global__ __launch_bounds__(512) void gemm_ceiling_kernel(int blocks, float* __
         f32x4 pp[2];
         pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], bq[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int q = 0; q < kMI * kWT; ++q) {
-            if (q + 1 < kMI * kWT)
+        for (int q = 0; q < kMI * kCeilWT; ++q) {
+            if (q + 1 < kMI * kCeilWT)
                 pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    a[(q + 1) / kWT], bq[(q + 1) % kWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    a[(q + 1) / kCeilWT], bq[(q + 1) % kCeilWT], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
+                acc[q / kCeilWT][q % kCeilWT][r] = fmaf(pp[q & 1][r], d[q % kCeilWT], acc[q / kCeilWT][q % kCeilWT][r]);
         }
     }
     float t = 0.0f;
 #pragma unroll
     for (int i = 0; i < kMI; ++i)
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
+        for (int j = 0; j < kCeilWT; ++j) t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
     if (t == 1234.5f) sink[0] = t;
 }
 
@@ -701,7 +753,7 @@ hipError_t launch_ceiling(int64_t m, int64_t n_tiles, int64_t k, float* sink, hi
     // the grid, workgroup and K split of launch_kind's two shapes
     const bool small = m <= kBMMax;
     const int bm = small ? 64 : 128, threads = small ? 512 : 256, parts = small ? 4 : 2;
-    const int64_t bt = 2 * kWT;  // weight tiles per workgroup (2 column slices)
+    const int64_t bt = 2 * kCeilWT;  // weight tiles per workgroup (2 column slices)
     const dim3 grid((unsigned)((n_tiles + bt - 1) / bt), (unsigned)((m + bm - 1) / bm));
     const int blocks = (int)((k / kQK + parts - 1) / parts);
     if (small)
@@ -735,6 +787,24 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+int gemm_shape(const Weight& w, int64_t m, bool split_x) {
+    switch (w.type) {
+    case OPENMINI_QMM_Q4_0:
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, true>())
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, false>());
+    case OPENMINI_QMM_Q8_0:
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, true>())
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, false>());
+    case OPENMINI_QMM_Q4_K:
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, true>())
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, false>());
+    case OPENMINI_QMM_Q6_K:
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, true>())
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, false>());
+    default: return -1;
+    }
 }
 
 size_t gemm_f32_workspace_bytes(int64_t m, int64_t k) {

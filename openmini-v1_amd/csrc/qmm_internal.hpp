@@ -225,6 +225,9 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
 // hi / lo parts plus a per-row exponent into `work` (gemm_f32_workspace_bytes(m, k)
 // bytes, 256-byte aligned), launch_gemm_split runs the GEMM on them.
 size_t gemm_f32_workspace_bytes(int64_t m, int64_t k);
+// The prefill GEMM's launch shape (0..3, qmm_gemm.hip choose_shape) for m rows of bf16
+// (split_x false) or split fp32 (true) activations; -1 for a type it does not take.
+int gemm_shape(const Weight& w, int64_t m, bool split_x);
 hipError_t split_rows(const float* x, int64_t m, int64_t k, void* work, hipStream_t s);
 hipError_t launch_gemm_split(const Weight& w, const void* work, int64_t m, float* y, hipStream_t s, bool gate_in_y);
 hipError_t launch_gemm_ceiling(int type, int64_t m, int64_t n, int64_t k, float* sink, hipStream_t s);

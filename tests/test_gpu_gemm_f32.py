@@ -222,3 +222,37 @@ def test_gemm_f32_workspace_checks(qmm):
     assert L.openmini_qmm_gemm_f32(w.handle, dx.ptr, dy.ptr, M, misaligned, need, None) == _native.ERR_INVALID_PARAM
     assert L.openmini_qmm_gemm_f32(w.handle, dx.ptr, dy.ptr, M, None, need, None) == _native.ERR_INVALID_PARAM
     assert L.openmini_qmm_gemm_f32_workspace_bytes(0, K) == 0
+
+
+@pytest.mark.parametrize("split_x", [False, True])
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0, Q4_K, Q6_K])
+def test_gemm_every_launch_shape(qmm, orc, qtype, split_x):
+    """The prefill GEMM picks one of four launch shapes (128 or 64 rows x 3 or 2 weight
+    tiles per wave) from the problem size.  Over these sizes every shape must be picked
+    at least once, for every weight type, with bf16 and with split fp32 activations,
+    and every call meets the oracle (sampled rows, y NaN-filled)."""
+    L = _native.lib()
+    K = 512
+    seen = {}
+    for N, M in ((100, 5), (4096, 512), (8192, 1024), (11008, 512), (11008, 128)):
+        blocks = blocks_for(qtype, N, K, seed=0xF70 + N + M)
+        w = qmm.QuantizedWeight(qtype, blocks, N, K)
+        shape = L.openmini_qmm_gemm_launch_shape(w.handle, M, int(split_x))
+        assert 0 <= shape <= 3, shape
+        print(f"gemm shape {shape}: type={qtype} split_x={split_x} N={N} M={M}", flush=True)
+        x = synth.normal(0xF71 + M, (M, K), 1.0)
+        rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(N).integers(0, M, 6)]))
+        if split_x:
+            y = run_gemm_f32(qmm, w, x)
+            ref = orc.linear_f64(qtype, blocks, N, K, x[rows])
+        else:
+            xb = synth.to_bf16_bits(x)
+            dx, dy = qmm.DeviceBuffer.from_numpy(xb), qmm.DeviceBuffer(M * N * 4)
+            dy.fill(0xFF)
+            w.gemm_bf16(dx, dy, M)
+            y = dy.download(np.float32, (M, N))
+            ref = orc.linear_bf16x_f64(qtype, blocks, N, K, xb[rows])
+        assert np.all(np.isfinite(y)), "unwritten (NaN) outputs"
+        assert_parity(y[rows], ref, TOL, f"shape {shape} N={N} M={M}")
+        seen.setdefault(shape, (N, M))
+    assert sorted(seen) == [0, 1, 2, 3], seen
