@@ -444,13 +444,40 @@ def bench_weight_path(qmm, hipr, stream, steps, warmup, N=11008, K=4096):
     chunk_bytes = ws[0].info().device_bytes
     for w in ws:
         w.close()
-    d_raw.free()
     alg = raw.size + chunk_bytes
     res["upload"] = {"workload": f"q4_0_upload_device_n{N}_k{K}", "unit": "GB/s",
                      "value": round(alg / (ms * 1e-3) / 1e9, 2), "us_per_call": round(ms * 1e3, 3),
                      "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": alg,
                      "includes": "the weight's hipMalloc and the repack kernel",
                      "sha256": {"gguf": sha256(raw)}}
+    # the same upload into caller memory (openmini_qmm_upload_device_into): one arena,
+    # no allocation per call, the repack alone; sources and destinations rotated past
+    # the MALL
+    per = (chunk_bytes + 255) // 256 * 256
+    srcs = [d_raw] + [qmm.DeviceBuffer.from_numpy(raw) for _ in range(3)]
+    arena = qmm.DeviceBuffer(per * reps)
+
+    def upload_into(i):
+        return qmm.QuantizedWeight.from_device_into(Q4_0, srcs[i % len(srcs)], raw.size, N, K, arena,
+                                                    (i % reps) * per, sh)
+
+    for i in range(3):
+        upload_into(i).close()  # a handle closes without touching the arena or the stream
+    stream.synchronize()
+    e0.record(sh)
+    ws = [upload_into(i) for i in range(reps)]
+    e1.record(sh)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    for w in ws:
+        w.close()
+    for b in srcs + [arena]:
+        b.free()
+    res["upload_into"] = {"workload": f"q4_0_upload_device_into_n{N}_k{K}", "unit": "GB/s",
+                          "value": round(alg / (ms * 1e-3) / 1e9, 2), "us_per_call": round(ms * 1e3, 3),
+                          "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": alg,
+                          "includes": "the repack kernel (caller-provided weight memory)",
+                          "sha256": {"gguf": sha256(raw)}}
     return res
 
 
@@ -672,6 +699,8 @@ def main(argv=None) -> int:
             log(f"dequantize {r['workload']}: {r['kernel_us']:.2f} us, {r['value']:.1f} GB/s")
         log(f"upload {wpath['upload']['workload']}: {wpath['upload']['us_per_call']:.2f} us per call, "
             f"{wpath['upload']['value']:.1f} GB/s")
+        log(f"upload {wpath['upload_into']['workload']}: {wpath['upload_into']['us_per_call']:.2f} us per call, "
+            f"{wpath['upload_into']['value']:.1f} GB/s")
     copy = None
     if args.calibrate_copy:
         copy = copy_calibration(qmm, hipr, stream)

@@ -146,6 +146,26 @@ int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_
                                int64_t n_rows, int64_t k_cols, void* stream,
                                openmini_qweight_t** out_weight);
 
+/* The device bytes a weight of this type and shape occupies (its chunks, then the
+ * batched GEMV's K-split workspace for weights that have one): what
+ * openmini_qmm_upload_device_into needs.  Errors as openmini_qmm_upload's shape checks.
+ * No counterpart in the reference (its loader allocates per tensor). */
+int openmini_qmm_weight_device_bytes(int type, int64_t n_rows, int64_t k_cols, size_t* out_bytes);
+
+/* openmini_qmm_upload_device into caller-owned device memory, with no device
+ * allocation: d_weight_mem (256-byte aligned, device memory of the current device, at
+ * least openmini_qmm_weight_device_bytes) holds the weight until
+ * openmini_qmm_free_weight, which then frees the handle only; the caller frees the
+ * memory after that.  For loaders that place a model's weights in one device arena
+ * (one allocation for every layer), where the upload is bound by the repack kernel.
+ * No counterpart in the reference (quant_loader.rs:54-138 keeps one allocation per
+ * tensor).  Errors: those of openmini_qmm_upload_device; INVALID_PARAM for memory
+ * that is null, unaligned, smaller than needed, or not on the current device. */
+int openmini_qmm_upload_device_into(int type, const void* d_gguf_blocks, size_t gguf_bytes,
+                                    int64_t n_rows, int64_t k_cols, void* d_weight_mem,
+                                    size_t weight_mem_bytes, void* stream,
+                                    openmini_qweight_t** out_weight);
+
 void openmini_qmm_free_weight(openmini_qweight_t* weight);
 
 int openmini_qmm_weight_info(const openmini_qweight_t* weight,

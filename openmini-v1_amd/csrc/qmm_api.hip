@@ -21,6 +21,8 @@ struct openmini_qweight {
     // launches go to the null stream, which orders them too; the lock keeps that
     // guarantee independent of the stream).
     mutable std::mutex batch_mu;
+    // false for openmini_qmm_upload_device_into: the caller's memory, not freed here
+    bool owns_memory = true;
 };
 
 namespace {
@@ -153,10 +155,8 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
     return OPENMINI_QMM_OK;
 }
 
-int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qweight** out) {
-    openmini_qweight* h = new (std::nothrow) openmini_qweight();
-    if (!h) return fail(OPENMINI_QMM_ERR_MEMORY, "host allocation failed");
-    qmm::Weight& w = h->w;
+// The weight's geometry and device size (chunks, then the K-split workspace).
+void plan_weight(int type, int64_t n_rows, int64_t k_cols, int dev, qmm::Weight& w) {
     w.type = type;
     w.device = dev;
     w.n = n_rows;
@@ -166,9 +166,26 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
     w.groups = (w.nb + qmm::kTileBlocks - 1) / qmm::kTileBlocks;
     w.chunk_bytes = (size_t)qmm::chunk_bytes(type);
     qmm::batch_split(type, w.n_tiles, w.groups, &w.split_t, &w.split_s);
+    w.device_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256) +
+                     qmm::split_workspace_bytes(w.n_tiles, w.split_t, w.split_s);
+}
+
+// Places a planned weight at `base` (device_bytes, 256-byte aligned).
+void bind_weight(qmm::Weight& w, void* base) {
+    w.chunks = static_cast<uint8_t*>(base);
     const size_t chunks_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256);
-    const size_t ws_bytes = qmm::split_workspace_bytes(w.n_tiles, w.split_t, w.split_s);
-    w.device_bytes = chunks_bytes + ws_bytes;
+    if (w.device_bytes > chunks_bytes) {
+        w.split_part = reinterpret_cast<float*>(w.chunks + chunks_bytes);
+        w.split_cnt = reinterpret_cast<uint32_t*>(
+            w.chunks + chunks_bytes + (size_t)w.split_s * qmm::kBatchRows * (size_t)w.n_tiles * qmm::kTileRows * 4);
+    }
+}
+
+int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qweight** out) {
+    openmini_qweight* h = new (std::nothrow) openmini_qweight();
+    if (!h) return fail(OPENMINI_QMM_ERR_MEMORY, "host allocation failed");
+    qmm::Weight& w = h->w;
+    plan_weight(type, n_rows, k_cols, dev, w);
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, w.device_bytes);
     if (e != hipSuccess) {
@@ -176,12 +193,7 @@ int alloc_weight(int type, int64_t n_rows, int64_t k_cols, int dev, openmini_qwe
         return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc(%zu) for weight failed: %s", w.device_bytes,
                     hipGetErrorString(e));
     }
-    w.chunks = static_cast<uint8_t*>(base);
-    if (ws_bytes) {
-        w.split_part = reinterpret_cast<float*>(w.chunks + chunks_bytes);
-        w.split_cnt = reinterpret_cast<uint32_t*>(
-            w.chunks + chunks_bytes + (size_t)w.split_s * qmm::kBatchRows * (size_t)w.n_tiles * qmm::kTileRows * 4);
-    }
+    bind_weight(w, base);
     *out = h;
     return OPENMINI_QMM_OK;
 }
@@ -390,9 +402,59 @@ int openmini_qmm_upload_device(int type, const void* d_gguf_blocks, size_t gguf_
     return ok();
 }
 
+int openmini_qmm_weight_device_bytes(int type, int64_t n_rows, int64_t k_cols, size_t* out_bytes) {
+    if (!out_bytes) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_bytes");
+    *out_bytes = 0;
+    const int rc = validate_weight_args(type, SIZE_MAX, n_rows, k_cols);  // the shape only
+    if (rc != OPENMINI_QMM_OK) return rc;
+    qmm::Weight w;
+    plan_weight(type, n_rows, k_cols, 0, w);
+    *out_bytes = w.device_bytes;
+    return ok();
+}
+
+int openmini_qmm_upload_device_into(int type, const void* d_gguf_blocks, size_t gguf_bytes, int64_t n_rows,
+                                    int64_t k_cols, void* d_weight_mem, size_t weight_mem_bytes, void* stream,
+                                    openmini_qweight_t** out_weight) {
+    if (!out_weight) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null out_weight");
+    *out_weight = nullptr;
+    int rc = validate_weight_args(type, gguf_bytes, n_rows, k_cols);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    if (!d_gguf_blocks) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null d_gguf_blocks");
+    if (!d_weight_mem || ((uintptr_t)d_weight_mem & 255u))
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "d_weight_mem must be a non-null 256-byte aligned device address");
+    int dev = 0;
+    rc = ensure_device(&dev);
+    if (rc != OPENMINI_QMM_OK) return rc;
+    openmini_qweight* h = new (std::nothrow) openmini_qweight();
+    if (!h) return fail(OPENMINI_QMM_ERR_MEMORY, "host allocation failed");
+    plan_weight(type, n_rows, k_cols, dev, h->w);
+    if (weight_mem_bytes < h->w.device_bytes) {
+        const size_t need = h->w.device_bytes;
+        delete h;
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "weight memory of %zu bytes, %zu needed", weight_mem_bytes, need);
+    }
+    hipPointerAttribute_t attr{};
+    if (hipPointerGetAttributes(&attr, d_weight_mem) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+        attr.device != dev) {
+        (void)hipGetLastError();
+        delete h;
+        return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "d_weight_mem is not device memory of the current device %d", dev);
+    }
+    bind_weight(h->w, d_weight_mem);
+    h->owns_memory = false;
+    hipError_t e = qmm::launch_repack(h->w, static_cast<const uint8_t*>(d_gguf_blocks), as_stream(stream));
+    if (e != hipSuccess) {
+        delete h;
+        return hip_fail(e, "repack launch");
+    }
+    *out_weight = h;
+    return ok();
+}
+
 void openmini_qmm_free_weight(openmini_qweight_t* weight) {
     if (!weight) return;
-    if (weight->w.chunks) {
+    if (weight->w.chunks && weight->owns_memory) {
         int cur = 0;
         const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != weight->w.device;
         if (switch_dev) (void)hipSetDevice(weight->w.device);

@@ -8,7 +8,7 @@
 //   f16 scale decode        quant.rs:166-167, 296-297 (half::f16::to_f32, exact)
 // Q4_0 GGUF byte j of a block holds element 2j in its HIGH nibble and element
 // 2j+1 in its LOW nibble (quant.rs:179-188); value = (q - 8) * f32(d).
-#include "qmm_internal.hpp"
+#include "qmm_device.hpp"
 
 namespace qmm {
 namespace {
@@ -21,82 +21,148 @@ __device__ __forceinline__ uint32_t q4_code(const uint8_t* qs, int e) {
     return (e & 1) ? (b & 0x0Fu) : (b >> 4);
 }
 
-// One workgroup writes kRepackChunks consecutive chunks of one row tile, whole: thread
-// t fills slot e = t % 64 of chunk t / 64 -- block 4 g + e / 16 of row 16 rt + e % 16 --
-// so each chunk's codes and scales leave as contiguous wave stores.  Slots outside the
-// weight (rows past n, blocks past nb: the tile padding) are written as zeros, so every
-// byte of the chunk array is written exactly once and no clearing pass is needed.
-// The workgroup's 16 rows x 16 blocks of GGUF bytes are staged through LDS with 16-byte
-// loads when they are all present and 16-byte aligned (nb % 8 == 0, aligned source);
-// otherwise each thread reads its own block with byte loads.
-template <int kBPB>
+// Q4_0 / Q8_0 blocks -> chunks.  A workgroup writes kRepackQuads x kRepackChunks
+// consecutive chunks of one row tile, whole: thread t fills slot e = t % 64 of chunk
+// t / 64 of each of its quads -- block 4 g + e / 16 of row 16 rt + e % 16 -- so each
+// chunk's codes and scales leave as contiguous wave stores.  Slots outside the weight
+// (rows past n, blocks past nb: the tile padding) are written as zeros, so every byte of
+// the chunk array is written exactly once and no clearing pass is needed.
+// When the workgroup's 16 rows are all present and start 16-byte aligned (nb % 8 == 0,
+// aligned source), their 16 kQuads blocks are copied to LDS by buffer loads with an LDS
+// destination, all issued before the first wait: one memory round trip per workgroup.
+// (Pieces past a row's last block hold the next row's bytes, or zeros past the source,
+// and are never used.)  Each slot then reads its block as 32-bit words and moves nibbles
+// with byte permutes.  Otherwise (the last row tile of a weight whose rows are not a
+// multiple of 16, or an unaligned source) each thread reads its own blocks with byte
+// loads.  Measured on MI355X, whole upload_device_into calls back to back, 11008 x 4096
+// Q4_0: copies through registers (a wait per copy) and a byte loop per slot 15.2 us,
+// with word reads 13.5 us, LDS-destination copies 10.2 (one quad per workgroup), 10.1
+// (two; Q8_0 19.4-19.6 us) and 14.0 us (four: too few workgroups in flight).
+template <int kBPB, int kQuads>
 __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* __restrict__ gguf, int64_t n,
-                                                                int64_t nb, int64_t groups, int64_t quads,
+                                                                int64_t nb, int64_t groups, int64_t wg_per_tile,
                                                                 int aligned16, uint8_t* __restrict__ chunks) {
     constexpr bool kQ4 = kBPB == 18;
     constexpr int kCB = kQ4 ? 16 : 32;
     constexpr int kChunk = chunk_bytes_for(kQ4);
-    constexpr int kRowB = kRepackChunks * kTileBlocks * kBPB;  // one row's bytes in the workgroup
-    constexpr int kPieces = kTileRows * kRowB / 16;
-    __shared__ uint4 tile[kPieces];
+    constexpr int kBlocks = kQuads * kRepackChunks * kTileBlocks;  // blocks of one row in the workgroup
+    constexpr int kRowB = kBlocks * kBPB;
+    constexpr int kSegs = kRowB / 16;                // 16-byte pieces of one row
+    constexpr int kPieces = kTileRows * kSegs;
+    constexpr int kPiecesPad = (kPieces + 63) / 64 * 64;  // whole waves of copies
+    static_assert(kRowB % 16 == 0, "rows of whole 16-byte pieces");
+    // one spare piece: a slot's word reads run up to 2 bytes past its block
+    __shared__ uint4 tile[kPiecesPad + 1];
     uint8_t* t8 = reinterpret_cast<uint8_t*>(tile);
 
-    const int64_t rt = (int64_t)blockIdx.x / quads, gq = (int64_t)blockIdx.x % quads;
-    const int64_t row0 = rt * kTileRows, blk0 = gq * kRepackChunks * kTileBlocks;
-    const bool staged = aligned16 && row0 + kTileRows <= n && blk0 + kRepackChunks * kTileBlocks <= nb;
+    const int64_t rt = (int64_t)blockIdx.x / wg_per_tile, wq = (int64_t)blockIdx.x % wg_per_tile;
+    const int64_t row0 = rt * kTileRows, blk0 = wq * kBlocks;
+    const bool staged = aligned16 && row0 + kTileRows <= n;
+    const int t = threadIdx.x;
     if (staged) {  // uniform per workgroup
-        for (int i = threadIdx.x; i < kPieces; i += kRepackThreads) {
-            const int r = i / (kRowB / 16), j = i % (kRowB / 16);
-            tile[i] = reinterpret_cast<const uint4*>(gguf + ((row0 + r) * nb + blk0) * kBPB)[j];
+        // 32-bit offsets: the source is smaller than the chunk array (< 4 GiB)
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(gguf, (uint32_t)(n * nb * kBPB));
+        const int wave = t >> 6, lane = t & 63;
+#pragma unroll
+        for (int p0 = wave * 64; p0 < kPieces; p0 += kRepackThreads) {  // p0 uniform per wave
+            const int p = p0 + lane, r = p / kSegs, j = p % kSegs;
+            // pieces past the last one (the padding of a wave) read zeros
+            const uint32_t off =
+                p < kPieces ? (uint32_t)(((row0 + r) * nb + blk0) * kBPB) + (uint32_t)j * 16u : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(t8 + p0 * 16), 16,
+                                                     off, 0, 0, 0);
         }
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this thread's copies have landed
         __syncthreads();
     }
-    const int t = threadIdx.x;
     const int c = t / kTileEntries, e = t % kTileEntries;
-    const int64_t grp = gq * kRepackChunks + c;
-    if (grp >= groups) return;
-    const int64_t row = row0 + (e & 15), blk = grp * kTileBlocks + (e >> 4);
-    uint8_t* chunk = chunks + (rt * groups + grp) * kChunk;
-    uint16_t scale = 0;
-    uint32_t w[kCB / 4];
+    const int64_t row = row0 + (e & 15);
 #pragma unroll
-    for (int j = 0; j < kCB / 4; ++j) w[j] = 0;
-    if (row < n && blk < nb) {
-        uint8_t b[kBPB];
-        if (staged) {
-            const uint8_t* src = t8 + (e & 15) * kRowB + (c * kTileBlocks + (e >> 4)) * kBPB;
+    for (int qq = 0; qq < kQuads; ++qq) {
+        const int64_t grp = (wq * kQuads + qq) * kRepackChunks + c;
+        if (grp >= groups) break;
+        const int64_t blk = grp * kTileBlocks + (e >> 4);
+        uint8_t* chunk = chunks + (rt * groups + grp) * kChunk;
+        uint16_t scale = 0;
+        uint32_t w[kCB / 4];
 #pragma unroll
-            for (int i = 0; i < kBPB; ++i) b[i] = src[i];
-        } else {
+        for (int j = 0; j < kCB / 4; ++j) w[j] = 0;
+        if (staged && blk < nb) {  // row < n holds for every slot of a staged workgroup
+            // The block starts 2-byte aligned (kBPB is even): the scale as one 16-bit
+            // read, the codes as 32-bit reads from the word boundary below them, realigned.
+            const int src = (e & 15) * kRowB + (int)(blk - blk0) * kBPB;
+            scale = *reinterpret_cast<const uint16_t*>(t8 + src);
+            const int a = src + 2, sh = a & 3;  // codes start; sh is 0 or 2
+            const uint32_t* a32 = reinterpret_cast<const uint32_t*>(t8 + (a - sh));
+            uint32_t v[kCB / 4 + 1];
+#pragma unroll
+            for (int j = 0; j <= kCB / 4; ++j) v[j] = a32[j];
+            uint32_t q[kCB / 4];  // code bytes 4 j .. 4 j + 3
+#pragma unroll
+            for (int j = 0; j < kCB / 4; ++j) q[j] = __builtin_amdgcn_alignbyte(v[j + 1], v[j], (uint32_t)sh);
+            if constexpr (kQ4) {
+                // code word j holds elements 8 j .. 8 j + 7: GGUF bytes s0..s3 = code bytes
+                // 4 j .. 4 j + 3 (element 2 m in the high nibble of s_m, 2 m + 1 in the
+                // low); chunk byte i = element 8 j + i | element 8 j + 4 + i << 4, i.e.
+                // bytes (s0.hi | s2.hi << 4, s0.lo | s2.lo << 4, s1.hi | s3.hi << 4,
+                // s1.lo | s3.lo << 4)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t pp = __builtin_amdgcn_perm(0u, q[j], 0x01010000u);  // s0 s0 s1 s1
+                    const uint32_t rr = __builtin_amdgcn_perm(0u, q[j], 0x03030202u);  // s2 s2 s3 s3
+                    const uint32_t lo = ((pp >> 4) & 0x000F000Fu) | (pp & 0x0F000F00u);
+                    const uint32_t hi = (rr & 0x00F000F0u) | ((rr << 4) & 0xF000F000u);
+                    w[j] = (lo | hi) ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) w[j] = q[j];
+            }
+        } else if (row < n && blk < nb) {
+            uint8_t b[kBPB];
             const uint8_t* src = gguf + (row * nb + blk) * kBPB;
 #pragma unroll
             for (int i = 0; i < kBPB; ++i) b[i] = src[i];
-        }
-        scale = (uint16_t)(b[0] | (b[1] << 8));
-        const uint8_t* qs = b + 2;
-        if constexpr (kQ4) {
+            scale = (uint16_t)(b[0] | (b[1] << 8));
+            const uint8_t* qs = b + 2;
+            if constexpr (kQ4) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t v = 0;
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t v = 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t lo = q4_code(qs, 8 * j + i);
-                    const uint32_t hi = q4_code(qs, 8 * j + 4 + i);
-                    v |= (lo | (hi << 4)) << (8 * i);
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t lo = q4_code(qs, 8 * j + i);
+                        const uint32_t hi = q4_code(qs, 8 * j + 4 + i);
+                        v |= (lo | (hi << 4)) << (8 * i);
+                    }
+                    w[j] = v ^ 0x88888888u;
                 }
-                w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
-            }
-        } else {
+            } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) | ((uint32_t)qs[4 * j + 2] << 16) |
-                       ((uint32_t)qs[4 * j + 3] << 24);
+                for (int j = 0; j < 8; ++j)
+                    w[j] = (uint32_t)qs[4 * j] | ((uint32_t)qs[4 * j + 1] << 8) | ((uint32_t)qs[4 * j + 2] << 16) |
+                           ((uint32_t)qs[4 * j + 3] << 24);
+            }
         }
+        reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = scale;
+        uint4* c4 = reinterpret_cast<uint4*>(chunk + e * kCB);
+        c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
     }
-    reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = scale;
-    uint4* c4 = reinterpret_cast<uint4*>(chunk + e * kCB);
-    c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// 16 GGUF code bytes of a slot as 32-bit words: from LDS byte address a (any
+// alignment) by word reads at the boundary below it, realigned.  Reads up to 3 bytes
+// past the 16 (within the staged span).
+template <int kWords>
+__device__ __forceinline__ void lds_words(const uint8_t* base, int a, uint32_t* q) {
+    const int sh = a & 3;
+    const uint32_t* a32 = reinterpret_cast<const uint32_t*>(base + (a - sh));
+    uint32_t v[kWords + 1];
+#pragma unroll
+    for (int j = 0; j <= kWords; ++j) v[j] = a32[j];
+#pragma unroll
+    for (int j = 0; j < kWords; ++j) q[j] = __builtin_amdgcn_alignbyte(v[j + 1], v[j], (uint32_t)sh);
 }
 
 // K-quant super-blocks -> chunks (layouts in qmm_internal.hpp).  A workgroup fills the
@@ -104,13 +170,19 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
 // 4q .. 4q + 3; a group is half a super-block); thread t fills slot t % 64 of chunk
 // t / 64, consecutive threads consecutive slots, so a wave writes a chunk's codes as one
 // contiguous span; every byte of the chunk array is written (padding rows as zeros).
-// Q6_K: a slot's 28 source bytes lie in three places of its super-block, so the 16 rows'
-// two super-blocks are first copied to LDS with coalesced 4-byte loads.  A row's span
-// may start at any byte: the loads run 4-byte aligned from a buffer resource based at
-// the source rounded down to 4 bytes, the source's last word is read byte by byte, and
-// nothing past the source is read.  Q4_K: a slot's 19 bytes are read straight from HBM
-// (measured faster than staging at 11008 x 4096: 16 vs 19 us; Q6_K staged 27 us, direct
-// 133-152 us).  Super-block reading as the reference's (paths relative to
+// A slot's source bytes lie in several places of its super-block (Q6_K: codes, high
+// bits, scales; Q4_K: codes, scale, d, dmin), so the 16 rows' two super-blocks are
+// first copied to LDS by 4-byte buffer loads with an LDS destination, all issued
+// before the first wait.  A row's span starts at any byte (210 is not a multiple of 4,
+// and device uploads may start anywhere): the copies run 4-byte aligned from a buffer
+// resource based at the source rounded down to 4 bytes; a word past the source reads
+// zero, and the source's last word, when partial, is re-read byte by byte, so nothing
+// past the source is read.  Each slot then takes its codes as 32-bit LDS words and
+// moves nibbles and 2-bit fields with byte permutes and masked shifts.  Measured on
+// MI355X at 11008 x 4096 (whole upload calls into caller memory): Q4_K 14.1 us and
+// Q6_K 20.3 us with register copies (a wait per copy, Q6_K) or byte loads from HBM
+// (Q4_K) and per-element byte loops.
+// Super-block reading as the reference's (paths relative to
 // openmini-server/src/model/inference/):
 //   Q4_K quant.rs:338-410: d = fp16 at 0, dmin = fp16 at 2, scale of sub-block sb =
 //        byte 4 + sb & 0x3F, codes from byte 12 (sub-block sb: 16 bytes at 12 + 16 sb,
@@ -131,36 +203,49 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
     constexpr int kDOff = kScaleOff + (kQ6 ? 2 : 1) * kTileEntries;
     constexpr int kSpan = 2 * kBPB;                // one row's bytes in the workgroup
     constexpr int kRowDw = (kSpan + 3 + 3) / 4;    // dwords that cover it from any start
+    constexpr int kWords = kTileRows * kRowDw;
+    constexpr int kWordsPad = (kWords + 63) / 64 * 64;  // whole waves of copies
     static_assert(kRepackChunks == 4, "a workgroup covers two super-blocks");
-    __shared__ uint32_t stage[kQ6 ? kTileRows * kRowDw : 1];
+    __shared__ uint32_t stage[kWordsPad];
+    const uint8_t* st8 = reinterpret_cast<const uint8_t*>(stage);
 
     const int64_t rt = (int64_t)blockIdx.x / quads, q = (int64_t)blockIdx.x % quads;
     const int64_t row0 = rt * kTileRows, s0 = 2 * q;
     const uint32_t delta = (uint32_t)((uintptr_t)gguf & 3u);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<void*>((uintptr_t)gguf & ~(uintptr_t)3), (short)0, (int)(src_bytes + delta), 0x00020000);
+    const uint64_t end = (uint64_t)src_bytes + delta;  // the source's end from the aligned base
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(reinterpret_cast<const void*>((uintptr_t)gguf & ~(uintptr_t)3), (uint32_t)end);
     // byte offset of row r's span from the aligned base (fits: src_bytes + 3 < 2^32)
     auto span_off = [&](int r) {
         return (uint32_t)(((row0 + r) * supers + s0) * kBPB) + delta;
     };
-    for (int i = threadIdx.x; kQ6 && i < kTileRows * kRowDw; i += kRepackThreads) {
+    auto word_off = [&](int i) -> uint64_t {  // source offset of staged word i
         const int r = i / kRowDw, j = i % kRowDw;
-        uint32_t v = 0;
-        if (row0 + r < n) {
-            const uint64_t a = (uint64_t)(span_off(r) & ~3u) + 4u * (uint32_t)j;
-            const uint64_t end = (uint64_t)src_bytes + delta;
-            if (a + 4 <= end) {
-                v = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)a, 0, 0);
-            } else {  // the source's last word may be partial: its bytes one by one
+        return (uint64_t)(span_off(r) & ~3u) + 4u * (uint32_t)j;
+    };
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-                for (uint32_t b = 0; b < 4; ++b)
-                    if (a + b < end)
-                        v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)(a + b), 0, 0) << (8 * b);
+    for (int i0 = wave * 64; i0 < kWords; i0 += kRepackThreads) {  // i0 uniform per wave
+        const int i = i0 + lane;
+        const uint64_t a = word_off(i);
+        const bool live = i < kWords && row0 + i / kRowDw < n && a + 4 <= end;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(stage + i0), 4,
+                                                 live ? (uint32_t)a : 0x80000000u, 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this thread's copies have landed
+    __syncthreads();
+    if ((end & 3u) != 0 && row0 + kTileRows >= n && s0 + 2 >= supers) {  // uniform: may hold the source's last word
+        for (int i = threadIdx.x; i < kWords; i += kRepackThreads) {
+            const uint64_t a = word_off(i);
+            if (row0 + i / kRowDw < n && a < end && a + 4 > end) {
+                uint32_t v = 0;
+                for (uint32_t b = 0; a + b < end; ++b)
+                    v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, (uint32_t)(a + b), 0, 0) << (8 * b);
+                stage[i] = v;
             }
         }
-        stage[i] = v;
+        __syncthreads();
     }
-    if constexpr (kQ6) __syncthreads();
 
     const int t = threadIdx.x, c = t / kTileEntries, e = t % kTileEntries, r = e & 15;
     const int64_t g = q * kRepackChunks + c;
@@ -172,56 +257,53 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
     uint32_t sc = 0;
     uint16_t dbits = 0;
     if (row < n) {
-        const uint8_t* blk =
-            kQ6 ? reinterpret_cast<const uint8_t*>(stage) + r * kRowDw * 4 + (span_off(r) & 3u) + (c >> 1) * kBPB
-                : gguf + (row * supers + s0 + (c >> 1)) * kBPB;
-        const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+        const int blk = r * kRowDw * 4 + (int)(span_off(r) & 3u) + (c >> 1) * kBPB;  // LDS byte address
+        const uint16_t d = (uint16_t)(st8[blk] | (st8[blk + 1] << 8));
+        uint32_t qw[4];
         if constexpr (!kQ6) {
-            uint8_t qs[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) qs[i] = blk[12 + sub * 16 + i];
+            lds_words<4>(st8, blk + 12 + sub * 16, qw);
+            // code word j: elements 8 j .. 8 j + 7 from GGUF bytes s0..s3 (element 2 m in
+            // the high nibble of s_m): chunk bytes (s0.hi | s2.hi << 4, s0.lo | s2.lo << 4,
+            // s1.hi | s3.hi << 4, s1.lo | s3.lo << 4), nibble q ^ 8 (two's-complement q - 8)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    v |= (q4_code(qs, 8 * j + i) | (q4_code(qs, 8 * j + 4 + i) << 4)) << (8 * i);
-                w[j] = v ^ 0x88888888u;  // nibble q ^ 8: the two's-complement value q - 8
+                const uint32_t pp = __builtin_amdgcn_perm(0u, qw[j], 0x01010000u);  // s0 s0 s1 s1
+                const uint32_t rr = __builtin_amdgcn_perm(0u, qw[j], 0x03030202u);  // s2 s2 s3 s3
+                const uint32_t lo = ((pp >> 4) & 0x000F000Fu) | (pp & 0x0F000F00u);
+                const uint32_t hi = (rr & 0x00F000F0u) | ((rr << 4) & 0xF000F000u);
+                w[j] = (lo | hi) ^ 0x88888888u;
             }
-            sc = blk[4 + sub] & 0x3Fu;
+            sc = st8[blk + 4 + sub] & 0x3Fu;
             // dmin * 0 is NaN for an inf / NaN dmin, and so is every value of the block
-            const uint16_t dmin = (uint16_t)(blk[2] | (blk[3] << 8));
+            const uint16_t dmin = (uint16_t)(st8[blk + 2] | (st8[blk + 3] << 8));
             dbits = (dmin & 0x7C00u) == 0x7C00u ? (uint16_t)0x7E00u : d;
         } else {
-            uint8_t ql[16], qh[8];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ql[i] = blk[2 + sub * 16 + i];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qh[i] = blk[66 + sub * 8 + i];
-            uint32_t lo4[32], hi2[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                lo4[i] = (i & 1) ? (ql[i >> 1] >> 4) : (ql[i >> 1] & 0x0Fu);
-                // v = q & 63 = low + 16 ((high + 2) & 3): the top bits are high ^ 2
-                hi2[i] = ((qh[i >> 2] >> ((i & 3) * 2)) & 3u) ^ 2u;
-            }
+            lds_words<4>(st8, blk + 2 + sub * 16, qw);
+            // low nibbles, element 2 m in the LOW nibble of s_m: chunk bytes
+            // (s0.lo | s2.lo << 4, s0.hi | s2.hi << 4, s1.lo | s3.lo << 4, s1.hi | s3.hi << 4)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v |= (lo4[8 * j + i] | (lo4[8 * j + 4 + i] << 4)) << (8 * i);
-                w[j] = v;
+                const uint32_t pp = __builtin_amdgcn_perm(0u, qw[j], 0x01010000u);
+                const uint32_t rr = __builtin_amdgcn_perm(0u, qw[j], 0x03030202u);
+                const uint32_t lo = (pp & 0x000F000Fu) | ((pp >> 4) & 0x0F000F00u);
+                const uint32_t hi = ((rr << 4) & 0x00F000F0u) | (rr & 0xF000F000u);
+                w[j] = lo | hi;
             }
+            // top bits: GGUF word m (bytes f = 0..3) holds elements 16 m + 4 f + i in bit
+            // pair i of byte f; the chunk wants them in bit pair f of byte i (a 4 x 4
+            // transpose of 2-bit fields), as high ^ 2 (v = q & 63 = low + 16 (high ^ 2))
+            uint32_t hw[2];
+            lds_words<2>(st8, blk + 66 + sub * 8, hw);
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int f = 0; f < 4; ++f) v |= hi2[16 * m + 4 * f + i] << (8 * i + 2 * f);
-                w[4 + m] = v;
+                uint32_t x = hw[m];
+                uint32_t tt = ((x >> 6) ^ x) & 0x00CC00CCu;
+                x ^= tt ^ (tt << 6);
+                tt = ((x >> 12) ^ x) & 0x0000F0F0u;
+                x ^= tt ^ (tt << 12);
+                w[4 + m] = x ^ 0xAAAAAAAAu;
             }
-            sc = (uint32_t)blk[130 + 2 * sub] | ((uint32_t)blk[131 + 2 * sub] << 8);
+            sc = (uint32_t)st8[blk + 130 + 2 * sub] | ((uint32_t)st8[blk + 131 + 2 * sub] << 8);
             dbits = d;
         }
     }
@@ -602,13 +684,16 @@ hipError_t launch_repack_chunks(const Weight& w, const uint8_t* gguf, hipStream_
     }
     const int aligned = ((uintptr_t)gguf % 16) == 0 && w.nb % 8 == 0;
     const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
-    const dim3 grid((unsigned)(w.n_tiles * quads));
-    if (w.type == OPENMINI_QMM_Q4_0)
-        hipLaunchKernelGGL(repack_kernel<18>, grid, dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups,
-                           quads, aligned, w.chunks);
-    else
-        hipLaunchKernelGGL(repack_kernel<34>, grid, dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups,
-                           quads, aligned, w.chunks);
+    constexpr int kQ4Quads = 2, kQ8Quads = 2;
+    if (w.type == OPENMINI_QMM_Q4_0) {
+        const int64_t per_tile = (quads + kQ4Quads - 1) / kQ4Quads;
+        hipLaunchKernelGGL((repack_kernel<18, kQ4Quads>), dim3((unsigned)(w.n_tiles * per_tile)),
+                           dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups, per_tile, aligned, w.chunks);
+    } else {
+        const int64_t per_tile = (quads + kQ8Quads - 1) / kQ8Quads;
+        hipLaunchKernelGGL((repack_kernel<34, kQ8Quads>), dim3((unsigned)(w.n_tiles * per_tile)),
+                           dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups, per_tile, aligned, w.chunks);
+    }
     return hipGetLastError();
 }
 

@@ -13,4 +13,4 @@ from .ops import (GEMM_MIN_ROWS, DeviceBuffer, GgufTensorType, HipQuantGemmEngin
                   get_gemm_engine, init, linear,
                   linear_gemm, safe_dequantize, safe_dequantize_q4_0, safe_dequantize_q4_1,
                   safe_dequantize_q8_0, stream_copy, stream_read,
-                  gemm_ceiling, gemm_f32_workspace)
+                  gemm_ceiling, gemm_f32_workspace, weight_device_bytes)

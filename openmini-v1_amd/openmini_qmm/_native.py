@@ -82,6 +82,8 @@ SIGNATURES = {
     "openmini_qmm_estimate_memory_usage": (_sz, [_i, _sz]),
     "openmini_qmm_upload": (_i, [_i, _p, _sz, _i64, _i64, ctypes.POINTER(_p)]),
     "openmini_qmm_upload_device": (_i, [_i, _p, _sz, _i64, _i64, _p, ctypes.POINTER(_p)]),
+    "openmini_qmm_weight_device_bytes": (_i, [_i, _i64, _i64, ctypes.POINTER(_sz)]),
+    "openmini_qmm_upload_device_into": (_i, [_i, _p, _sz, _i64, _i64, _p, _sz, _p, ctypes.POINTER(_p)]),
     "openmini_qmm_free_weight": (None, [_p]),
     "openmini_qmm_weight_info": (_i, [_p, ctypes.POINTER(WeightInfo)]),
     "openmini_qmm_gemv": (_i, [_p, _p, _p, _i64, _p]),

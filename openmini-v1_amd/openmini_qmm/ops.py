@@ -196,6 +196,24 @@ class QuantizedWeight:
         self.n_rows, self.k_cols = int(n_rows), int(k_cols)
         return self
 
+    @classmethod
+    def from_device_into(cls, tensor_type: int, d_blocks: DeviceBuffer, nbytes: int, n_rows: int,
+                         k_cols: int, d_mem: DeviceBuffer, offset: int = 0, stream=None) -> "QuantizedWeight":
+        """Uploads into caller memory: `offset` bytes into `d_mem` (256-byte aligned),
+        weight_device_bytes(...) long (openmini_qmm_upload_device_into).  The weight
+        must be closed before d_mem is freed."""
+        if offset < 0 or offset % 256:
+            raise InvalidInput(f"offset {offset} is not a non-negative multiple of 256")
+        self = cls.__new__(cls)
+        self.handle = ctypes.c_void_p()
+        check(lib().openmini_qmm_upload_device_into(int(tensor_type), d_blocks.ptr, int(nbytes), int(n_rows),
+                                                    int(k_cols), ctypes.c_void_p(d_mem.ptr.value + offset),
+                                                    max(0, d_mem.nbytes - offset), stream,
+                                                    ctypes.byref(self.handle)))
+        self.tensor_type = GgufTensorType(int(tensor_type))
+        self.n_rows, self.k_cols = int(n_rows), int(k_cols)
+        return self
+
     def info(self) -> _native.WeightInfo:
         info = _native.WeightInfo()
         check(lib().openmini_qmm_weight_info(self.handle, ctypes.byref(info)))
@@ -230,6 +248,14 @@ class QuantizedWeight:
             self.close()
         except Exception:
             pass
+
+
+def weight_device_bytes(tensor_type: int, n_rows: int, k_cols: int) -> int:
+    """Device bytes an uploaded weight of this type and shape occupies
+    (openmini_qmm_weight_device_bytes): the size QuantizedWeight.from_device_into needs."""
+    out = ctypes.c_size_t()
+    check(lib().openmini_qmm_weight_device_bytes(int(tensor_type), int(n_rows), int(k_cols), ctypes.byref(out)))
+    return int(out.value)
 
 
 def gemm_f32_workspace(m: int, k_cols: int) -> DeviceBuffer:

@@ -95,6 +95,8 @@ extern "C" {
     pub fn openmini_qmm_estimate_memory_usage(tensor_type: c_int, n_elements: usize) -> usize;
     pub fn openmini_qmm_upload(tensor_type: c_int, gguf_blocks: *const c_void, gguf_bytes: usize, n_rows: i64, k_cols: i64, out_weight: *mut *mut QWeight) -> c_int;
     pub fn openmini_qmm_upload_device(tensor_type: c_int, d_gguf_blocks: *const c_void, gguf_bytes: usize, n_rows: i64, k_cols: i64, stream: *mut c_void, out_weight: *mut *mut QWeight) -> c_int;
+    pub fn openmini_qmm_weight_device_bytes(tensor_type: c_int, n_rows: i64, k_cols: i64, out_bytes: *mut usize) -> c_int;
+    pub fn openmini_qmm_upload_device_into(tensor_type: c_int, d_gguf_blocks: *const c_void, gguf_bytes: usize, n_rows: i64, k_cols: i64, d_weight_mem: *mut c_void, weight_mem_bytes: usize, stream: *mut c_void, out_weight: *mut *mut QWeight) -> c_int;
     pub fn openmini_qmm_free_weight(weight: *mut QWeight);
     pub fn openmini_qmm_weight_info(weight: *const QWeight, info: *mut WeightInfo) -> c_int;
     pub fn openmini_qmm_gemv(weight: *const QWeight, d_x: *const f32, d_y: *mut f32, batch: i64, stream: *mut c_void) -> c_int;

@@ -36,8 +36,8 @@ def random_blocks(qtype, nblocks, seed, finite=True):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
-@pytest.mark.parametrize("shape", [(1, 32), (3, 96), (37, 4160), (256, 4096), (4096, 4096),
-                                   (11008, 4096), (4096, 11008)])
+@pytest.mark.parametrize("shape", [(1, 32), (3, 96), (37, 4160), (37, 4096), (256, 4096), (4096, 4096),
+                                   (11008, 4096), (4096, 11008), (1000, 11008)])
 def test_upload_then_dequant_is_bit_exact(qmm, orc, qtype, shape):
     N, K = shape
     print(f"dequant_weight type={qtype} N={N} K={K}", flush=True)
@@ -210,6 +210,74 @@ def test_upload_from_device_any_alignment(qmm, orc, qtype, offset):
     got = w.dequantize()
     ref = orc.dequantize(qtype, blocks, N * K).reshape(N, K)
     assert np.array_equal(bits(got), bits(ref))
+
+
+def test_upload_device_into_one_arena(qmm, orc):
+    """openmini_qmm_upload_device_into: three weights (Q4_0, a Q8_0 with a K-split
+    workspace, a Q4_K) placed back to back in one caller allocation at 256-byte
+    boundaries.  Each dequantizes bit-exactly, and its GEMV at 1 and 8 rows equals the
+    same weight uploaded with its own allocation, bit for bit.  Closing the handles
+    leaves the arena to the caller, which then reuses it for another weight."""
+    specs = [(Q4_0, 1000, 4096, 0xD00), (Q8_0, 4096, 11008, 0xD01), (12, 777, 2048, 0xD02)]
+    sizes = [qmm.weight_device_bytes(t, n, k) for t, n, k, _ in specs]
+    offsets = np.cumsum([0] + [(b + 255) // 256 * 256 for b in sizes])
+    arena = qmm.DeviceBuffer(int(offsets[-1]))
+    arena.fill(0xA5)  # stale bytes: the repack and the split-counter clear must cover them
+    own, placed = [], []
+    for (t, n, k, seed), off, size in zip(specs, offsets, sizes):
+        blocks = synth.kquant_blocks(t, n, k, seed=seed) if t == 12 else synth.weight_blocks(t, n, k, seed=seed)
+        d = qmm.DeviceBuffer.from_numpy(blocks)
+        w = qmm.QuantizedWeight.from_device_into(t, d, blocks.size, n, k, arena, int(off))
+        ref = qmm.QuantizedWeight(t, blocks, n, k)
+        assert w.info().device_bytes == ref.info().device_bytes == size
+        if t != 12:
+            assert np.array_equal(bits(w.dequantize()), bits(orc.dequantize(t, blocks, n * k).reshape(n, k)))
+        own.append(ref)
+        placed.append(w)
+    for (t, n, k, seed), w, ref in zip(specs, placed, own):
+        for b in (1, 8):
+            print(f"upload_into type={t} N={n} K={k} b={b}", flush=True)
+            x = qmm.DeviceBuffer.from_numpy(synth.normal(seed + b, (b, k), 1.0))
+            ya, yb = qmm.DeviceBuffer(b * n * 4), qmm.DeviceBuffer(b * n * 4)
+            w.gemv(x, ya, b)
+            ref.gemv(x, yb, b)
+            assert np.array_equal(ya.download(np.float32, (b, n)).view(np.uint32),
+                                  yb.download(np.float32, (b, n)).view(np.uint32))
+    for w in placed:
+        w.close()
+    t, n, k, seed = specs[0]
+    blocks = synth.weight_blocks(t, n, k, seed=seed + 7)
+    w = qmm.QuantizedWeight.from_device_into(t, qmm.DeviceBuffer.from_numpy(blocks), blocks.size, n, k, arena,
+                                             int(offsets[1]))
+    assert np.array_equal(bits(w.dequantize()), bits(orc.dequantize(t, blocks, n * k).reshape(n, k)))
+    w.close()
+    arena.free()
+
+
+def test_upload_device_into_rejects_bad_memory(qmm):
+    """Memory that is unaligned, too small, or host memory is rejected with
+    INVALID_PARAM and no handle."""
+    import ctypes
+    from openmini_qmm import _native
+    L = _native.lib()
+    N, K = 64, 1024
+    blocks = synth.weight_blocks(Q4_0, N, K, seed=0xD10)
+    d = qmm.DeviceBuffer.from_numpy(blocks)
+    need = qmm.weight_device_bytes(Q4_0, N, K)
+    arena = qmm.DeviceBuffer(need + 512)
+    h = ctypes.c_void_p()
+    host = np.zeros(need + 256, np.uint8)
+    host_ptr = ctypes.c_void_p((host.ctypes.data + 255) // 256 * 256)
+    for mem, size, what in ((ctypes.c_void_p(arena.ptr.value + 128), need, b"aligned"),
+                            (arena.ptr, need - 1, b"needed"), (host_ptr, need, b"device memory"),
+                            (ctypes.c_void_p(), need, b"aligned")):
+        rc = L.openmini_qmm_upload_device_into(Q4_0, d.ptr, blocks.size, N, K, mem, size, None, ctypes.byref(h))
+        assert rc == _native.ERR_INVALID_PARAM and not h.value, (rc, what)
+        assert what in L.openmini_qmm_last_error(), L.openmini_qmm_last_error()
+    out = ctypes.c_size_t()
+    assert L.openmini_qmm_weight_device_bytes(Q4_0, N, K + 1, ctypes.byref(out)) == _native.ERR_INVALID_PARAM
+    assert out.value == 0
+    arena.free()
 
 
 def test_gpu_quant_ops_mirror(qmm, orc):
