@@ -420,12 +420,20 @@ hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, 
 
 // K slices per row tile (phases of 4 groups).  One batch row: W = 8 or 16, whichever
 // pads the last phases with fewer groups (ties: 16, more waves); measured on MI355X,
-// e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  More batch rows: at most 8 (LDS and
-// registers per wave grow with the batch).  Short K: the most slices that keep 4
-// groups per wave.
+// e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  Nibble codes on at most 512 row tiles
+// (two workgroups per CU or fewer) with K of 64+ groups: 16 waves of 2-group phases,
+// twice the waves in flight (two interleaved passes, Q4_0: 4096 x 11008 7.25-7.58 ->
+// 7.03-7.14 us, 8192 x 28672 26.7-27.3 -> 25.5-25.6, 8192 x 8192 8.40-8.51 ->
+// 8.31-8.36; Q8_0 4096 x 11008 lost 10% and 4096 x 4096 (32 groups) gained nothing).
+// Fewer, longer waves lose at the headline shape: 11008 x 4096 Q4_0 W = 8 6.29-6.33
+// us, W = 4 (8-group phases) 6.64-6.67, W = 2 8.02-8.10.
+// More batch rows: at most 8 (LDS and registers per wave grow with the batch).  Short
+// K: the most slices that keep 4 groups per wave.
 template <int kFmt, int B, int kKind>
 hipError_t run_w(const GemvGroup& grp, int64_t g, int64_t k, const float* x, hipStream_t s) {
     if (g >= 32) {
+        if constexpr (B == 1 && Fmt<kFmt>::kNib)
+            if (g >= 64 && grp.tile_begin[kMaxGroup] <= 512) return run<kFmt, B, 16, 2, kKind>(grp, g, k, x, s);
         if constexpr (B == 1) {
             const int64_t pad16 = (g + 63) / 64 * 64 - g, pad8 = (g + 31) / 32 * 32 - g;
             if (pad16 <= pad8) return run<kFmt, B, 16, 4, kKind>(grp, g, k, x, s);
