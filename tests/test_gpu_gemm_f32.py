@@ -46,9 +46,10 @@ def linear_host(w, x):
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0, Q4_K, Q6_K])
 @pytest.mark.parametrize("N,K,M", [(16, 256, 1), (100, 512, 5), (130, 1024, 64), (257, 2304, 200),
-                                   (640, 512, 384)])
+                                   (640, 512, 384), (64, 6144, 130), (48, 11008, 129)])
 def test_gemm_f32_shapes(qmm, orc, qtype, N, K, M):
-    """Ragged N and M, both tile shapes (M <= 128 and above), every weight type."""
+    """Ragged N and M, both tile shapes (M <= 128 and above), every weight type, K from
+    256 to 11008."""
     print(f"gemm_f32 type={qtype} N={N} K={K} M={M}", flush=True)
     blocks = blocks_for(qtype, N, K, seed=0xF00 + N + K + M)
     x = synth.normal(0xF01 + M, (M, K), 1.0)
