@@ -40,6 +40,25 @@ __device__ __forceinline__ f16x8 codes_q4(uint32_t w) {
     return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
 }
 
+// The same 8 codes in the element order (0, 2, 1, 3, 4, 6, 5, 7), one operation fewer
+// per pair: nibble positions 0 / 4 (elements 0, 2) and 2 / 6 (1, 3) become the fp16
+// 1024 + (n ^ 8) = 1024 + q by one bit-field select each (magic bits from both
+// constants, bit 3 of the nibble inverted, bits 0-2 kept); positions 1 / 5 (4, 6) and
+// 3 / 7 (5, 7) likewise as 1024 + 16 q, scaled by 1/16 in the packed fma that removes
+// the offset (exact: 64 + q - 72).  A caller feeds the activations in the same order.
+__device__ __forceinline__ f16x8 codes_q4_perm(uint32_t w) {
+    constexpr uint32_t kC0 = 0x64076407u, kB0 = 0x64086408u;  // low nibbles of each half
+    constexpr uint32_t kC1 = 0x64706470u, kB1 = 0x64806480u;  // high nibbles of each half
+    const uint32_t w8 = w >> 8;
+    const uint32_t h0 = (w & kC0) | (~w & kB0), h1 = (w8 & kC0) | (~w8 & kB0);
+    const uint32_t h2 = (w & kC1) | (~w & kB1), h3 = (w8 & kC1) | (~w8 & kB1);
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f}, c72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const f16x2 v2 = __builtin_bit_cast(f16x2, h2) * s16 + c72, v3 = __builtin_bit_cast(f16x2, h3) * s16 + c72;
+    uint32_t p[4] = {pk_sub(h0, (_Float16)1032.0f), pk_sub(h1, (_Float16)1032.0f), __builtin_bit_cast(uint32_t, v2),
+                     __builtin_bit_cast(uint32_t, v3)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
 // 8 Q8_0 codes (two words, int8) -> 8 fp16 q.
 __device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
     const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128

@@ -8,7 +8,11 @@
 // Arithmetic (every product exact, fp32 accumulation):
 //   * Codes are exact in fp16: Q4_0 / Q4_K as q - 8, Q8_0 as q, Q6_K as q in
 //     [-32, 31].  They are built from the code bytes with the 1024 + u pattern
-//     (0x64XX is the fp16 1024 + XX, spacing 1) and one packed fp16 subtraction.
+//     (0x64XX is the fp16 1024 + XX, spacing 1) and one packed fp16 subtraction;
+//     nibbles by bit-field selects in the element order (0, 2, 1, 3, 4, 6, 5, 7),
+//     in which the activations are then loaded (9 VALU per 8 codes against 12 in
+//     order: 8192 x 8192 b = 16 18.8-19.6 -> 17.2-18.0 us, 11008 x 4096 b = 8
+//     12.0-12.2 -> 11.4 us, Q4_K b = 8 12.4-12.5 -> 11.7-12.1 us).
 //   * K-quant weights (the reference's reading, quant.rs:338-410 and :515-600) use
 //     their 32-element sub-blocks as the blocks, with block factor d * scale (exact).
 //     Q6_K's scale changes every 16 elements, inside one MFMA's 32: each half runs its
@@ -245,8 +249,13 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             const uint32_t off = x_lane + (ge < x_lim ? (uint32_t)ge * 4u : 0x80000000u);
             const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off, 0, 0));
             const float4 b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(x_rs, off + 16u, 0, 0));
-            st.x[tt][0] = a.x; st.x[tt][1] = a.y; st.x[tt][2] = a.z; st.x[tt][3] = a.w;
-            st.x[tt][4] = b.x; st.x[tt][5] = b.y; st.x[tt][6] = b.z; st.x[tt][7] = b.w;
+            if constexpr (F::kNib) {  // codes_q4_perm's element order
+                st.x[tt][0] = a.x; st.x[tt][1] = a.z; st.x[tt][2] = a.y; st.x[tt][3] = a.w;
+                st.x[tt][4] = b.x; st.x[tt][5] = b.z; st.x[tt][6] = b.y; st.x[tt][7] = b.w;
+            } else {
+                st.x[tt][0] = a.x; st.x[tt][1] = a.y; st.x[tt][2] = a.z; st.x[tt][3] = a.w;
+                st.x[tt][4] = b.x; st.x[tt][5] = b.y; st.x[tt][6] = b.z; st.x[tt][7] = b.w;
+            }
         }
 #pragma unroll
         for (int i = 0; i < kNT; ++i) {
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             for (int t = 0; t < 4; ++t) {
                 f16x8 b;
                 if constexpr (F::kNib)
-                    b = codes_q4(e[t]);
+                    b = codes_q4_perm(e[t]);  // the activations were loaded in its order
                 else if constexpr (F::kQ6K)
                     b = codes_q6(e[t], o[t], kq);
                 else
