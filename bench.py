@@ -36,8 +36,8 @@ sys.path.insert(0, os.path.join(ROOT, "openmini-v1_amd"))
 METRIC = "Q4_0 GEMV HBM GB/s (% of peak) at 4096x11008 b=1; Q8_0 GEMM TFLOP/s M=512"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 7, 12, 14
-TYPE_NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 7, 12, 13, 14
+TYPE_NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", Q4_1: "q4_1", Q5_K: "q5_k"}
 MALL_DEFEAT_BYTES = 1 << 30
 SUSTAINED_LAUNCHES = 500  # back-to-back launches of the sustained-load figures
 # the Llama-70B-style q / gate / down projections (N, K, seed),
@@ -94,7 +94,7 @@ def weight_blocks(qtype, N, K, seed, sigma=0.02):
     from openmini_qmm import synth
     key = (qtype, N, K, seed, sigma)
     if key not in _BLOCKS:
-        _BLOCKS[key] = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q6_K)
+        _BLOCKS[key] = (synth.kquant_blocks(qtype, N, K, seed=seed) if qtype in (Q4_K, Q5_K, Q6_K)
                         else synth.weight_blocks(qtype, N, K, seed=seed, sigma=sigma))
     return _BLOCKS[key]
 
@@ -682,9 +682,14 @@ def main(argv=None) -> int:
     if not args.no_shapes:
         # decode GEMV on K-quant weights (Llama-7B up / down shapes at batch 1; the up
         # shape at batch 8 through the batched kernel)
+        # and on the block-minimum types Q4_1 and Q5_K (GGUF bytes counted: Q5_K's chunks
+        # hold its 5-bit codes in the 6-bit Q6_K form, 27% above them)
         for qtype, n, k, b, seed in ((Q4_K, 11008, 4096, 1, 0x5EED0071), (Q4_K, 4096, 11008, 1, 0x5EED0072),
                                      (Q6_K, 11008, 4096, 1, 0x5EED0073), (Q6_K, 4096, 11008, 1, 0x5EED0074),
-                                     (Q4_K, 11008, 4096, 8, 0x5EED0075), (Q6_K, 11008, 4096, 8, 0x5EED0076)):
+                                     (Q4_K, 11008, 4096, 8, 0x5EED0075), (Q6_K, 11008, 4096, 8, 0x5EED0076),
+                                     (Q4_1, 11008, 4096, 1, 0x5EED0077), (Q4_1, 4096, 11008, 1, 0x5EED0078),
+                                     (Q5_K, 11008, 4096, 1, 0x5EED0079), (Q4_1, 11008, 4096, 8, 0x5EED007A),
+                                     (Q5_K, 11008, 4096, 8, 0x5EED007B)):
             r = bench_gemv(qmm, hipr, stream, max(20, args.steps // 2), max(5, args.warmup // 2), N=n, K=k,
                            qtype=qtype, batch=b, seed=seed)
             kquant.append({"workload": f"{TYPE_NAME[qtype]}_gemv_n{n}_k{k}_b{b}", "unit": "GB/s",

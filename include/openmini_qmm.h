@@ -56,9 +56,10 @@ typedef enum {
     OPENMINI_QMM_ERR_NOT_FOUND = -12     /* "Tensor not found" / missing metadata key */
 } openmini_qmm_status_t;
 
-/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload, the
- * decode GEMV and the prefill GEMM take Q4_0, Q8_0, Q4_K and Q6_K; the dequantization
- * entry points take every id listed. */
+/* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload and the
+ * decode GEMV take Q4_0, Q4_1, Q8_0, Q4_K, Q5_K and Q6_K; the prefill GEMM the same
+ * without Q4_1 and Q5_K (their blocks carry a minimum); the dequantization entry points
+ * take every id listed. */
 typedef enum {
     OPENMINI_QMM_F32 = 0,
     OPENMINI_QMM_F16 = 1,
@@ -80,8 +81,8 @@ typedef struct {
     int32_t type;            /* openmini_qmm_type_t */
     int32_t device;          /* HIP device ordinal holding the weight */
     int64_t n_rows;          /* N: output features */
-    int64_t k_cols;          /* K: input features, a multiple of 32 (256 for Q4_K / Q6_K) */
-    int64_t blocks_per_row;  /* K / 32 (32-element sub-blocks for Q4_K / Q6_K) */
+    int64_t k_cols;          /* K: input features, a multiple of 32 (256 for Q4_K / Q5_K / Q6_K) */
+    int64_t blocks_per_row;  /* K / 32 (32-element sub-blocks for the K-quants) */
     size_t gguf_bytes;       /* GGUF data_size: N * K / 32 * 18 | 34, N * K / 256 * 144 | 210 */
     size_t device_bytes;     /* HBM held by the handle */
 } openmini_qmm_weight_info_t;
@@ -134,8 +135,11 @@ size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
  * quantized and repacks them on the GPU for its access pattern.
  * Types: Q4_0, Q8_0, Q4_K and Q6_K (GEMV and GEMM; Q4_K / Q6_K with the reference's
  * own reading of those blocks, quant.rs:338-410 and :515-600, whose values are exact
- * products of an integer code and an fp32 sub-block factor).
- * Errors: INVALID_PARAM (k_cols % 32, or % 256 for Q4_K / Q6_K; sizes <= 0),
+ * products of an integer code and an fp32 sub-block factor); Q4_1 and Q5_K (GEMV only:
+ * q * d + m, quant.rs:216-262, and the reference's Q5_K reading (q - 16) * d * scale +
+ * dmin * minimum, quant.rs:433-505; each block's product gains its minimum times the
+ * block's activation sum).
+ * Errors: INVALID_PARAM (k_cols % 32, or % 256 for the K-quants; sizes <= 0),
  * UNSUPPORTED (type), INSUFFICIENT_DATA (gguf_bytes < required). */
 int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes,
                         int64_t n_rows, int64_t k_cols, openmini_qweight_t** out_weight);
@@ -197,7 +201,8 @@ int openmini_qmm_gemv(const openmini_qweight_t* weight, const float* d_x, float*
 /* Prefill GEMM: y[m, N] = x[m, K] . W^T with bf16 activations (raw bf16 bits),
  * fp32 output, on bf16 MFMA with exact integer codes and fp32 per-block scales.
  * Q4_0, Q8_0, Q4_K and Q6_K weights (Q6_K: code * 16-element scale, an exact integer,
- * as two bf16 parts, then the fp32 d).  d_x must be 16-byte aligned. */
+ * as two bf16 parts, then the fp32 d); UNSUPPORTED for Q4_1 / Q5_K, which run the
+ * decode GEMVs at any row count.  d_x must be 16-byte aligned. */
 int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x, float* d_y,
                            int64_t m, void* stream);
 
@@ -255,8 +260,8 @@ int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_
 
 /* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
  * fp32 in/out, synchronous.  Below 128 rows the decode GEMVs, from 128 rows on the
- * fp32 prefill GEMM (openmini_qmm_gemm_f32); x, y and the GEMM's workspace are
- * allocated per call. */
+ * fp32 prefill GEMM (openmini_qmm_gemm_f32; Q4_1 / Q5_K weights: the batched GEMV at
+ * any row count); x, y and the GEMM's workspace are allocated per call. */
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,
                              int64_t m);
 
@@ -264,10 +269,10 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  x and y are staged through a
  * fixed 16 MiB device array that the library holds on every device it runs on until
- * the process ends: x, then (from 128 rows on) the fp32 GEMM's workspace, then y, each
- * from a 256-byte boundary.  About m * (K + N) * 4 bytes below 128 rows and
- * m * (2 K + N + 1) * 4 from 128 rows on must fit in 16 MiB, else INVALID_PARAM naming
- * the row limit.  Same kernels and results as openmini_qmm_linear_host, synchronous
+ * the process ends: x, then (from 128 rows on, for the types the GEMM takes) the fp32
+ * GEMM's workspace, then y, each from a 256-byte boundary.  About m * (K + N) * 4
+ * bytes without the GEMM and m * (2 K + N + 1) * 4 with it must fit in 16 MiB, else
+ * INVALID_PARAM naming the row limit.  Same kernels and results as openmini_qmm_linear_host, synchronous
  * on the null stream.
  * All calls on one device share the array: the library holds a per-device lock from
  * the copy in to the copy out, so calls from several threads are safe and run one at
@@ -280,7 +285,7 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
 
 /* Dequantizes an uploaded Q4_0 / Q8_0 weight to f32 W[N, K] (row-major) in device memory
  * (d_out 16-byte aligned).  Bit-identical to quant::dequantize of the original GGUF bytes.
- * UNSUPPORTED for Q4_K / Q6_K handles: their GGUF bytes dequantize through
+ * UNSUPPORTED for the other weight types: their GGUF bytes dequantize through
  * openmini_qmm_dequantize_any_device. */
 int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, void* stream);
 
@@ -400,8 +405,8 @@ int openmini_qmm_gguf_get_string(const openmini_qmm_gguf_t* gguf, const char* ke
 
 /* QuantizedWeightLoader::load_tensor (quant_loader.rs:66-92) without dequantization: the
  * 2-D tensor [ne0 = K, ne1 = N] becomes the weight W[N, K] (row n = K consecutive
- * elements, the semantic layout linear() multiplies by); Q4_0 / Q8_0 / Q4_K / Q6_K (UNSUPPORTED
- * otherwise).  Copy and repack run on `stream`, synchronised before returning. */
+ * elements, the semantic layout linear() multiplies by); the weight types of
+ * openmini_qmm_upload (UNSUPPORTED otherwise).  Copy and repack run on `stream`, synchronised before returning. */
 int openmini_qmm_gguf_upload_weight(const openmini_qmm_gguf_t* gguf, const char* name, void* stream,
                                     openmini_qweight_t** out_weight);
 

@@ -72,11 +72,20 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
-// Weight layouts of the upload, the decode GEMV and the prefill GEMM; dequant_weight
-// takes Q4_0 and Q8_0.
+// Weight layouts of the upload and the decode GEMV; the prefill GEMM takes those
+// without a block minimum (not Q4_1 / Q5_K), dequant_weight Q4_0 and Q8_0.
 bool type_supported(int type) {
-    return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0 || qmm::is_kquant(type);
+    return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_1 || type == OPENMINI_QMM_Q8_0 ||
+           qmm::is_kquant(type);
 }
+int check_gemm_type(const qmm::Weight& w) {
+    if (qmm::has_block_min(w.type))
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
+                    "no prefill GEMM for type %d (Q4_1 / Q5_K weights run the decode GEMVs at any row count)", w.type);
+    return OPENMINI_QMM_OK;
+}
+// Rows that linear() hands to the fp32 prefill GEMM rather than the decode GEMVs.
+bool gemm_rows(const qmm::Weight& w, int64_t m) { return m >= qmm::kGemmMinRows && !qmm::has_block_min(w.type); }
 bool plain_type(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
 // quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
 bool safe_type(int type) {
@@ -128,8 +137,8 @@ size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_cols) {
     if (!type_supported(type))
-        return fail(OPENMINI_QMM_ERR_UNSUPPORTED, "unsupported tensor type %d (Q4_0=2, Q8_0=7, Q4_K=12, Q6_K=14)",
-                    type);
+        return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
+                    "unsupported tensor type %d (Q4_0=2, Q4_1=3, Q8_0=7, Q4_K=12, Q5_K=13, Q6_K=14)", type);
     if (n_rows <= 0 || k_cols <= 0)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "invalid shape [%lld, %lld]", (long long)n_rows,
                     (long long)k_cols);
@@ -496,6 +505,8 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
     if (!d_x || !d_y) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or y");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    rc = check_gemm_type(weight->w);
+    if (rc != OPENMINI_QMM_OK) return rc;
     hipError_t e = qmm::launch_gemm_bf16(weight->w, d_x, d_y, m, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return ok();
@@ -519,6 +530,8 @@ namespace {
 // Shared checks of the fp32-activation GEMM entry points.
 int check_f32_gemm_args(const qmm::Weight& w, const float* d_x, const void* d_out, int64_t m, const void* d_work,
                         size_t work_bytes) {
+    const int rc = check_gemm_type(w);
+    if (rc != OPENMINI_QMM_OK) return rc;
     if (!d_x || !d_out || !d_work) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x, output or workspace");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
@@ -613,6 +626,8 @@ int openmini_qmm_ffn_gate_up_bf16(const openmini_qweight_t* gate, const openmini
     if (!d_x || !d_h) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null x or h");
     if (m <= 0 || m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     if (!aligned16(d_x)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "x must be 16-byte aligned");
+    rc = check_gemm_type(gate->w);
+    if (rc != OPENMINI_QMM_OK) return rc;
     hipError_t e = qmm::launch_gemm_bf16(gate->w, d_x, d_h, m, as_stream(stream), false);
     if (e == hipSuccess) e = qmm::launch_gemm_bf16(up->w, d_x, d_h, m, as_stream(stream), true);
     if (e != hipSuccess) return hip_fail(e, "ffn_gate_up_bf16 launch");
@@ -634,10 +649,11 @@ int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_
 }
 
 namespace {
-// linear(x, W) on device buffers: the decode GEMVs below qmm::kGemmMinRows rows, else the
-// fp32-activation prefill GEMM (its workspace at d_work).
+// linear(x, W) on device buffers: the decode GEMVs below qmm::kGemmMinRows rows (and for
+// block-minimum types at any count), else the fp32-activation prefill GEMM (its
+// workspace at d_work).
 hipError_t linear_rows(const qmm::Weight& w, const float* dx, float* dy, int64_t m, void* d_work) {
-    if (m >= qmm::kGemmMinRows) {
+    if (gemm_rows(w, m)) {
         hipError_t e = qmm::split_rows(dx, m, w.k, d_work, nullptr);
         return e == hipSuccess ? qmm::launch_gemm_split(w, d_work, m, dy, nullptr, false) : e;
     }
@@ -652,10 +668,10 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
     if (m <= 0) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld must be >= 1", (long long)m);
     const qmm::Weight& w = weight->w;
     std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
-    if (w.split_s > 1 && m < qmm::kGemmMinRows && qmm::use_batch_kernel(w, m)) lk.lock();
+    if (w.split_s > 1 && !gemm_rows(w, m) && qmm::use_batch_kernel(w, m)) lk.lock();
     if (m > INT32_MAX) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "m=%lld out of range", (long long)m);
     const size_t xb = round_up((size_t)m * w.k * sizeof(float), 256), yb = (size_t)m * w.n * sizeof(float);
-    const size_t wb = m >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
+    const size_t wb = gemm_rows(w, m) ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, xb + wb + yb);
     if (e != hipSuccess) return fail(OPENMINI_QMM_ERR_MEMORY, "hipMalloc for linear_host failed: %s", hipGetErrorString(e));
@@ -678,7 +694,7 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
     const qmm::Weight& w = weight->w;
     // staging: x, the GEMM's workspace (from kGemmMinRows rows on), y, each 256-aligned
     auto staged_bytes = [&](int64_t rows) {
-        const size_t wb = rows >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(rows, w.k) : 0;
+        const size_t wb = gemm_rows(w, rows) ? qmm::gemm_f32_workspace_bytes(rows, w.k) : 0;
         return round_up((size_t)rows * w.k * sizeof(float), 256) + wb + (size_t)rows * w.n * sizeof(float);
     };
     if (m > INT32_MAX || staged_bytes(m) > kScratchBytes) {
@@ -695,9 +711,9 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
     if (rc != OPENMINI_QMM_OK) return rc;
     std::lock_guard<std::mutex> staging(g_staging_mu[w.device]);
     std::unique_lock<std::mutex> lk(weight->batch_mu, std::defer_lock);
-    if (w.split_s > 1 && m < qmm::kGemmMinRows && qmm::use_batch_kernel(w, m)) lk.lock();
+    if (w.split_s > 1 && !gemm_rows(w, m) && qmm::use_batch_kernel(w, m)) lk.lock();
     const size_t xb = round_up((size_t)m * w.k * sizeof(float), 256), yb = (size_t)m * w.n * sizeof(float);
-    const size_t wb = m >= qmm::kGemmMinRows ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
+    const size_t wb = gemm_rows(w, m) ? qmm::gemm_f32_workspace_bytes(m, w.k) : 0;
     float* dx = reinterpret_cast<float*>(base);
     uint8_t* work = base + xb;
     float* dy = reinterpret_cast<float*>(work + wb);

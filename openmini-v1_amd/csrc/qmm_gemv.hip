@@ -78,6 +78,16 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
     return v;
 }
 
+// Sum over the 16 lanes of a row, the same butterfly with adds (every lane ends with
+// the same value: each step adds the same two operands in both lanes of a pair).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __uint_as_float(dpp<kDppXor1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kDppXor2>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kDppMirror>(__float_as_uint(v)));
+    return v;
+}
+
 // Sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), in every
 // lane, with the gfx950 row swaps (registers only, no LDS round trip).  Each step adds
 // the same two values in every lane of a row pair, so the result is the one of
@@ -136,13 +146,18 @@ constexpr int kOne = 0, kGroup = 1, kPair = 2;
 // power of two the int8 code bytes carry (Q4_0 / Q4_K codes are 16 (q - 8), Q6_K 4 q).
 template <int kFmt>
 struct Fmt {
-    static constexpr bool kNib = kFmt == OPENMINI_QMM_Q4_0 || kFmt == OPENMINI_QMM_Q4_K;  // 16 B of nibbles
-    static constexpr bool kQ6 = kFmt == OPENMINI_QMM_Q6_K;
+    static constexpr bool kQ41 = kFmt == OPENMINI_QMM_Q4_1;
+    static constexpr bool kQ5 = kFmt == OPENMINI_QMM_Q5_K;
+    static constexpr bool kNib = kFmt == OPENMINI_QMM_Q4_0 || kFmt == OPENMINI_QMM_Q4_K || kQ41;  // 16 B of nibbles
+    static constexpr bool kQ6 = kFmt == OPENMINI_QMM_Q6_K || kQ5;                        // Q6_K chunk layout
     static constexpr bool kKQ = kFmt == OPENMINI_QMM_Q4_K || kQ6;                        // K-quant
+    static constexpr bool kMin = kQ41 || kQ5;                                            // block minimum
     static constexpr int kCB = kNib ? 16 : kQ6 ? 24 : 32;
     static constexpr int kCodeBytes = kTileEntries * kCB;
     static constexpr int kChunk = kFmt == OPENMINI_QMM_Q4_K ? kQ4KChunk
+                                  : kQ5                     ? kQ5KChunk
                                   : kQ6                     ? kQ6KChunk
+                                  : kQ41                    ? kQ41Chunk
                                                             : chunk_bytes_for(kFmt == OPENMINI_QMM_Q4_0);
     static constexpr int kDOff = kCodeBytes + (kQ6 ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
     static constexpr int kCodeShift = kNib ? 4 : kQ6 ? 2 : 0;
@@ -236,6 +251,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
         uint2 hb[kNW][P];      // Q6_K: the slot's 8 bytes of top code bits
         uint32_t sc[kNW][P];   // the slot's scale: fp16 bits (Q4_0 / Q8_0), u8 (Q4_K), 2 x int8 (Q6_K)
         uint32_t dk[kNW][P];   // K-quant: the row's fp16 d
+        uint32_t mn[kNW][P];   // block minimum: Q4_1 the slot's fp16 m, Q5_K its minimum nibble
+        uint32_t dm[kNW][P];   // Q5_K: the row's fp16 dmin
         // activations first: L2 hits that land before the weights do.  The whole offset
         // goes in the VGPR operand: the raw-buffer range check covers the VGPR offset
         // but not the SGPR one, so elements past k (a last group of fewer than 4
@@ -271,11 +288,18 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                     sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kCodeBytes + lane * 2, soff, 0);
                 if constexpr (F::kKQ)
                     dk[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], F::kDOff + ln * 2, soff, 0);
+                if constexpr (F::kQ41)
+                    mn[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kQ41MinOff + lane * 2, soff, 0);
+                if constexpr (F::kQ5) {
+                    mn[nw][p] = __builtin_amdgcn_raw_buffer_load_b8(w_rs[nw], kQ5KMinOff + lane, soff, 0);
+                    dm[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kQ5KDminOff + ln * 2, soff, 0);
+                }
             }
         }
 
         // digits of the phase's activation blocks -> LDS, while the chunks are in flight
         int shift[P][B];
+        float bsum[P][B];  // block minimum: the sum of the lane's block of activations
 #pragma unroll
         for (int p = 0; p < P; ++p)
 #pragma unroll
@@ -284,6 +308,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                 const uint32_t mb = row16_max(max(__float_as_uint(x0) & 0x7FFFFFFFu,
                                                   __float_as_uint(x1) & 0x7FFFFFFFu));
                 seen[b] = max(seen[b], mb);
+                if constexpr (F::kMin) bsum[p][b] = row16_sum(x0 + x1);
                 // 2^(e-1) <= max < 2^e with e = biased exponent - 126; s = 30 - e
                 shift[p][b] = 156 - (int)(mb >> 23);
                 // X = round(x * 2^s), |X| < 2^30 (x * 2^s is an integer from 2^23 up);
@@ -348,6 +373,11 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                     d0 = f16_bits_to_f32((uint16_t)sc[nw][p]);
                 }
                 d0 = live ? d0 : 0.0f;
+                // block minimum offset: Q4_1 (q - 8) d + (8 d + m); Q5_K dmin * minimum
+                float mo = 0.0f;
+                if constexpr (F::kQ41) mo = fmaf(8.0f, d0, f16_bits_to_f32((uint16_t)mn[nw][p]));
+                if constexpr (F::kQ5) mo = f16_bits_to_f32((uint16_t)dm[nw][p]) * (float)mn[nw][p];
+                mo = live ? mo : 0.0f;
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
                     const int base = (p * B + b) * 2 * kHalfSlots;
@@ -362,10 +392,12 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                         const i32x4 D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, i32x4{0, 0, 0, 0}, 0, 0, 0);
                         acc[nw][b] = fmaf(d0, __builtin_amdgcn_ldexpf(digit_sum(D0), sh), acc[nw][b]);
                         acc[nw][b] = fmaf(d1, __builtin_amdgcn_ldexpf(digit_sum(D1), sh), acc[nw][b]);
+                        if constexpr (F::kMin) acc[nw][b] = fmaf(mo, bsum[p][b], acc[nw][b]);
                     } else {
                         i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
                         D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, D, 0, 0, 0);
                         acc[nw][b] = fmaf(d0, __builtin_amdgcn_ldexpf(digit_sum(D), sh), acc[nw][b]);
+                        if constexpr (F::kMin) acc[nw][b] = fmaf(mo, bsum[p][b], acc[nw][b]);
                     }
                 }
             }
@@ -489,6 +521,8 @@ hipError_t launch_gemv_group(const Weight* const* ws, float* const* ys, int coun
     case OPENMINI_QMM_Q8_0: return dispatch_kind<OPENMINI_QMM_Q8_0>(grp, w0, x, batch, count, swiglu, s);
     case OPENMINI_QMM_Q4_K: return dispatch_kind<OPENMINI_QMM_Q4_K>(grp, w0, x, batch, count, swiglu, s);
     case OPENMINI_QMM_Q6_K: return dispatch_kind<OPENMINI_QMM_Q6_K>(grp, w0, x, batch, count, swiglu, s);
+    case OPENMINI_QMM_Q4_1: return dispatch_kind<OPENMINI_QMM_Q4_1>(grp, w0, x, batch, count, swiglu, s);
+    case OPENMINI_QMM_Q5_K: return dispatch_kind<OPENMINI_QMM_Q5_K>(grp, w0, x, batch, count, swiglu, s);
     default: return hipErrorInvalidValue;
     }
 }

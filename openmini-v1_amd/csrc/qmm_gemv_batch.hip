@@ -94,6 +94,14 @@ __device__ __forceinline__ float quarter_max(float m) {
 }
 
 
+// Sum over the same four lanes (every lane ends with the same value).
+__device__ __forceinline__ float quarter_sum(float m) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Register transposes across the four 16-lane rows of a wave (gfx950 row swaps:
 // permlane32_swap exchanges rows 2, 3 of its first operand with rows 0, 1 of its
 // second; permlane16_swap rows 1, 3 of the first with rows 0, 2 of the second).
@@ -147,13 +155,17 @@ template <int kFmt>
 struct BFmt {
     static constexpr bool kQ8 = kFmt == OPENMINI_QMM_Q8_0;
     static constexpr bool kQ4K = kFmt == OPENMINI_QMM_Q4_K;
-    static constexpr bool kQ6K = kFmt == OPENMINI_QMM_Q6_K;
+    static constexpr bool kQ41 = kFmt == OPENMINI_QMM_Q4_1;
+    static constexpr bool kQ5 = kFmt == OPENMINI_QMM_Q5_K;
+    static constexpr bool kQ6K = kFmt == OPENMINI_QMM_Q6_K || kQ5;  // Q6_K chunk layout
     static constexpr bool kKQ = kQ4K || kQ6K;
-    static constexpr bool kNib = !kQ8 && !kQ6K;  // Q4_0 / Q4_K: the codes are nibbles q ^ 8
+    static constexpr bool kMin = kQ41 || kQ5;    // block minimum
+    static constexpr bool kNib = !kQ8 && !kQ6K;  // Q4_0 / Q4_1 / Q4_K: the codes are nibbles q ^ 8
     static constexpr int kCB = kQ8 ? 32 : 16;      // bytes of a slot's (low) codes
     static constexpr int kScaleOff = kTileEntries * (kQ6K ? 24 : kCB);
     static constexpr int kDOff = kScaleOff + (kQ6K ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
-    static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ6K ? kQ6KChunk : chunk_bytes_for(!kQ8);
+    static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ5 ? kQ5KChunk : kQ6K ? kQ6KChunk : kQ41 ? kQ41Chunk
+                                                                                          : chunk_bytes_for(!kQ8);
 };
 
 template <int kFmt, int kNT, int kXB>
@@ -163,6 +175,8 @@ struct Stage {
     uint2 hb[BFmt<kFmt>::kQ6K ? kNT : 1];  // Q6_K: the slot's top code bits
     uint32_t sc[kNT];
     uint32_t dk[BFmt<kFmt>::kKQ ? kNT : 1];  // K-quant: the fp16 d of the slot's row
+    uint32_t mn[BFmt<kFmt>::kMin ? kNT : 1];  // Q4_1: the slot's fp16 m; Q5_K: its minimum nibble
+    uint32_t dm[BFmt<kFmt>::kQ5 ? kNT : 1];   // Q5_K: the fp16 dmin of the slot's row
 };
 
 // Q6_K low-nibble word kq and top-bit word kq / 2 of a slot -> 8 fp16 q, elements
@@ -205,7 +219,8 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     // per wave: the 16 A rows' 2^-s of the current group while running, then the
     // partial sums [W][kNT][64 lanes][4] for the reduction
     constexpr int kRed = W * kNT * 256;
-    constexpr int kScale = W * 16;
+    // per wave: 16 range scales, then (block minimum) 4 blocks x 16 activation-block sums
+    constexpr int kScale = W * 16 + (F::kMin ? W * 64 : 0);
     __shared__ __attribute__((aligned(16))) float lds[kRed > kScale ? kRed : kScale];
 
     const int lane = threadIdx.x & 63;
@@ -236,6 +251,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         ((uint32_t)min(li % kPartRows, batch - 1) * (uint32_t)k + (uint32_t)(part * kXB * 32 + kq * 8)) * 4u;
     const int x_lim = k - part * kXB * 32;  // slot element offset g * 128 + 32 tt must be below
     float* my_scale = lds + wave * 16;
+    float* my_sums = lds + W * 16 + wave * 64;  // [block][batch row]; block-minimum formats
 
     f32x4 acc[kNT];
 #pragma unroll
@@ -274,6 +290,11 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                 st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, F::kScaleOff + lane * 2, soff, 0);
             if constexpr (F::kKQ)  // the d of slot lane's row, lane % 16
                 st.dk[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, F::kDOff + li * 2, soff, 0);
+            if constexpr (F::kQ41) st.mn[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, kQ41MinOff + lane * 2, soff, 0);
+            if constexpr (F::kQ5) {
+                st.mn[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, kQ5KMinOff + lane, soff, 0);
+                st.dm[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, kQ5KDminOff + li * 2, soff, 0);
+            }
         }
     };
 
@@ -291,6 +312,18 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         // 2^e <= m < 2^(e+1), e = biased exponent - 127; s = 14 - e
         const int sh = 141 - (int)(__float_as_uint(m) >> 23);
         if (kq == 0) my_scale[li] = __builtin_amdgcn_ldexpf(1.0f, -sh);
+        if constexpr (F::kMin) {
+            // the sums of the lane's activation blocks (the lane's 8 elements, then the
+            // four k quarters), one lane per (batch row, block) writing
+#pragma unroll
+            for (int tt = 0; tt < kXB; ++tt) {
+                float v = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v += st.x[tt][j];
+                v = quarter_sum(v);
+                if (kq == 0) my_sums[((li / kPartRows) * kXB + tt) * 16 + li % kPartRows] = v;
+            }
+        }
         f16x8 ah[4], al[4];  // A operands of blocks 0..3 for the batch rows' lanes
 #pragma unroll
         for (int tt = 0; tt < kXB; ++tt) split8(st.x[tt], sh, ah[tt], al[tt]);
@@ -312,6 +345,13 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // 2^-s of the four A rows this lane's D values belong to (rows 4 kq .. 4 kq + 3)
         const f32x4 rs = *reinterpret_cast<const f32x4*>(my_scale + kq * 4);
+        // block minimum: the activation-block sums of those rows' batch rows, 4 kq + r
+        // modulo the rows per part (A rows repeat the batch rows)
+        f32x4 bs[4];
+        if constexpr (F::kMin) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bs[t] = *reinterpret_cast<const f32x4*>(my_sums + t * 16 + (kq * 4) % kPartRows);
+        }
 #pragma unroll
         for (int i = 0; i < kNT; ++i) {
             // lane (kq, i) takes word kq (Q4_0) / words 2 kq, 2 kq + 1 (Q8_0) of slot
@@ -344,6 +384,12 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             } else {
                 broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
             }
+            // block minimum offsets of column i's slots: Q4_1 (q - 8) d + (8 d + m),
+            // Q5_K dmin * minimum
+            float os[4];
+            if constexpr (F::kQ41)
+                broadcast4(fmaf(8.0f, f16_bits_to_f32((uint16_t)st.sc[i]), f16_bits_to_f32((uint16_t)st.mn[i])), os);
+            if constexpr (F::kQ5) broadcast4(f16_bits_to_f32((uint16_t)st.dm[i]) * (float)st.mn[i], os);
             f32x4 gs = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -375,6 +421,12 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(gs[r], rs[r], acc[i][r]);
+            if constexpr (F::kMin) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(os[t], bs[t][r], acc[i][r]);
+            }
         }
         // the next group rewrites my_scale after these reads (in-order LDS per wave)
     };
@@ -527,7 +579,7 @@ constexpr int64_t kCUs = 256;  // MI355X compute units
 
 static int64_t tiles_per_cu(int type, int64_t n_tiles, bool pair) {
     // a pair holds two weights' registers per tile: at most 4 / 3 tiles
-    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K;
+    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q4_1;
     const int64_t cap = pair ? (nib ? 4 : 3) : nib ? 8 : 4;
     const int64_t per_cu = (n_tiles + kCUs - 1) / kCUs;
     return per_cu < 1 ? 1 : per_cu > cap ? cap : per_cu;
@@ -547,7 +599,7 @@ static int64_t tiles_per_cu(int type, int64_t n_tiles, bool pair) {
 // depends on the shape only, so results stay bitwise independent of the batch size.
 void batch_split(int type, int64_t n_tiles, int64_t groups, int* t, int* s) {
     const int64_t t0 = tiles_per_cu(type, n_tiles, false);
-    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K;
+    const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q4_1;
     *t = (int)t0;
     *s = 1;
     if (groups < 32) return;  // at least 16 groups per split
@@ -651,6 +703,12 @@ hipError_t launch_gemv_batch(const Weight& w, const Weight* up, const float* x, 
     case OPENMINI_QMM_Q6_K:
         return up ? dispatch_rep<OPENMINI_QMM_Q6_K, 2>(w, w1, x, y, batch, sh, s)
                   : dispatch_rep<OPENMINI_QMM_Q6_K, 1>(w, w1, x, y, batch, sh, s);
+    case OPENMINI_QMM_Q4_1:
+        return up ? dispatch_rep<OPENMINI_QMM_Q4_1, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q4_1, 1>(w, w1, x, y, batch, sh, s);
+    case OPENMINI_QMM_Q5_K:
+        return up ? dispatch_rep<OPENMINI_QMM_Q5_K, 2>(w, w1, x, y, batch, sh, s)
+                  : dispatch_rep<OPENMINI_QMM_Q5_K, 1>(w, w1, x, y, batch, sh, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -44,6 +44,19 @@
 //     (word m, byte i, bits 2f..2f+1: element 16m + 4f + i); then 64 x 2 int8 scales
 //     (the slot's two 16-element halves); then 16 x fp16 d.  1696 B per chunk.
 //     (w << 2) & 0x3C3C3C3C | (hi << s) & 0xC0C0C0C0 is then 4 q per int8 byte.
+//
+// Types with a per-block minimum (their matmul adds min * (sum of the block's
+// activations) to each block's product):
+//   Q4_1 (20-byte blocks, quant.rs:216-262): element value q * d + m, q in [0, 15].
+//     Slot codes as Q4_0 (the nibble q ^ 8, i.e. q - 8) and fp16 scales d, then 64 x
+//     fp16 m: the value is (q - 8) * d + (8 d + m).  1280 B per chunk.
+//   Q5_K (176-byte super-blocks, the reference's reading quant.rs:433-505): element i
+//     of sub-block sb has q = (nibble of byte 36 + 16 sb + i / 2, even i high) + 16 *
+//     (bit i % 8 of byte 20 + sb) and value (q - 16) * d * (byte 4 + sb & 0x3F) +
+//     dmin * (nibble sb % 2 of byte 12 + sb / 2).  Stored as a Q6_K chunk whose 6-bit
+//     code is q - 16 (low nibble q & 15, top bits 0 or 3) with the sub-block scale in
+//     both halves, then 16 x fp16 dmin (per row) and 64 x u8 minimum nibbles.  The
+//     code term is exact as (q - 16) * (d * scale).  1792 B per chunk.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -80,21 +93,24 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// GGUF block geometry of the weight layouts (upload, GEMV; the GEMM takes Q4_0 and
-// Q8_0 only): elements and bytes per GGUF block.
-inline int weight_block_elems(int type) {
-    return (type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q6_K) ? 256 : 32;
+// GGUF block geometry of the weight layouts (upload, GEMV; the GEMM takes the types
+// without a block minimum): elements and bytes per GGUF block.
+inline bool is_kquant(int type) {
+    return type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q5_K || type == OPENMINI_QMM_Q6_K;
 }
+inline bool has_block_min(int type) { return type == OPENMINI_QMM_Q4_1 || type == OPENMINI_QMM_Q5_K; }
+inline int weight_block_elems(int type) { return is_kquant(type) ? 256 : 32; }
 inline int bytes_per_block(int type) {
     switch (type) {
     case OPENMINI_QMM_Q4_0: return 18;
+    case OPENMINI_QMM_Q4_1: return 20;
     case OPENMINI_QMM_Q8_0: return 34;
     case OPENMINI_QMM_Q4_K: return 144;
+    case OPENMINI_QMM_Q5_K: return 176;
     case OPENMINI_QMM_Q6_K: return 210;
     default: return 0;
     }
 }
-inline bool is_kquant(int type) { return type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q6_K; }
 
 // GgufTensorType::{block_size, bytes_per_block} (src/model/inference/gguf.rs:348-379)
 // for the layouts the dequantization entry points accept; 0 for others.
@@ -132,9 +148,21 @@ __host__ __device__ constexpr int chunk_bytes_for(bool q4) { return kTileEntries
 // K-quant chunks: codes, per-slot scale bytes, then one fp16 d per tile row.
 constexpr int kQ4KChunk = kTileEntries * 16 + kTileEntries + 2 * kTileRows;       // 1120
 constexpr int kQ6KChunk = kTileEntries * 24 + 2 * kTileEntries + 2 * kTileRows;   // 1696
+// Block-minimum chunks: Q4_1 = a Q4_0 chunk + 64 fp16 m; Q5_K = a Q6_K chunk + 16 fp16
+// dmin (per row) + 64 u8 minimum nibbles.
+constexpr int kQ41MinOff = kTileEntries * 16 + 2 * kTileEntries;                    // 1152
+constexpr int kQ41Chunk = kQ41MinOff + 2 * kTileEntries;                            // 1280
+constexpr int kQ5KDminOff = kQ6KChunk;                                              // 1696
+constexpr int kQ5KMinOff = kQ5KDminOff + 2 * kTileRows;                             // 1728
+constexpr int kQ5KChunk = kQ5KMinOff + kTileEntries;                                // 1792
 inline int chunk_bytes(int type) {
-    return type == OPENMINI_QMM_Q4_K ? kQ4KChunk : type == OPENMINI_QMM_Q6_K ? kQ6KChunk
-                                                                           : chunk_bytes_for(type == OPENMINI_QMM_Q4_0);
+    switch (type) {
+    case OPENMINI_QMM_Q4_K: return kQ4KChunk;
+    case OPENMINI_QMM_Q6_K: return kQ6KChunk;
+    case OPENMINI_QMM_Q5_K: return kQ5KChunk;
+    case OPENMINI_QMM_Q4_1: return kQ41Chunk;
+    default: return chunk_bytes_for(type == OPENMINI_QMM_Q4_0);
+    }
 }
 
 // Chunk index and slot of (row, blk).

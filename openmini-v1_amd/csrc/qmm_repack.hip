@@ -38,13 +38,17 @@ __device__ __forceinline__ uint32_t q4_code(const uint8_t* qs, int e) {
 // Q4_0: copies through registers (a wait per copy) and a byte loop per slot 15.2 us,
 // with word reads 13.5 us, LDS-destination copies 10.2 (one quad per workgroup), 10.1
 // (two; Q8_0 19.4-19.6 us) and 14.0 us (four: too few workgroups in flight).
+// Q4_1 (20-byte blocks: d, m, then the Q4_0 nibble order) takes the same path with its
+// codes stored as Q4_0's and m in the chunk's trailing fp16 array.
 template <int kBPB, int kQuads>
 __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* __restrict__ gguf, int64_t n,
                                                                 int64_t nb, int64_t groups, int64_t wg_per_tile,
                                                                 int aligned16, uint8_t* __restrict__ chunks) {
-    constexpr bool kQ4 = kBPB == 18;
+    constexpr bool kQ4 = kBPB != 34;                  // nibble codes: Q4_0, Q4_1
+    constexpr bool kMin = kBPB == 20;                 // Q4_1: fp16 m after d
     constexpr int kCB = kQ4 ? 16 : 32;
-    constexpr int kChunk = chunk_bytes_for(kQ4);
+    constexpr int kCodeOff = kBPB - kCB;              // codes end the block
+    constexpr int kChunk = kMin ? kQ41Chunk : chunk_bytes_for(kQ4);
     constexpr int kBlocks = kQuads * kRepackChunks * kTileBlocks;  // blocks of one row in the workgroup
     constexpr int kRowB = kBlocks * kBPB;
     constexpr int kSegs = kRowB / 16;                // 16-byte pieces of one row
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
         if (grp >= groups) break;
         const int64_t blk = grp * kTileBlocks + (e >> 4);
         uint8_t* chunk = chunks + (rt * groups + grp) * kChunk;
-        uint16_t scale = 0;
+        uint16_t scale = 0, minv = 0;
         uint32_t w[kCB / 4];
 #pragma unroll
         for (int j = 0; j < kCB / 4; ++j) w[j] = 0;
@@ -92,7 +96,8 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
             // read, the codes as 32-bit reads from the word boundary below them, realigned.
             const int src = (e & 15) * kRowB + (int)(blk - blk0) * kBPB;
             scale = *reinterpret_cast<const uint16_t*>(t8 + src);
-            const int a = src + 2, sh = a & 3;  // codes start; sh is 0 or 2
+            if constexpr (kMin) minv = *reinterpret_cast<const uint16_t*>(t8 + src + 2);
+            const int a = src + kCodeOff, sh = a & 3;  // codes start; sh is 0 or 2
             const uint32_t* a32 = reinterpret_cast<const uint32_t*>(t8 + (a - sh));
             uint32_t v[kCB / 4 + 1];
 #pragma unroll
@@ -124,7 +129,8 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
 #pragma unroll
             for (int i = 0; i < kBPB; ++i) b[i] = src[i];
             scale = (uint16_t)(b[0] | (b[1] << 8));
-            const uint8_t* qs = b + 2;
+            if constexpr (kMin) minv = (uint16_t)(b[2] | (b[3] << 8));
+            const uint8_t* qs = b + kCodeOff;
             if constexpr (kQ4) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -145,6 +151,7 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kernel(const uint8_t* _
             }
         }
         reinterpret_cast<uint16_t*>(chunk + kTileEntries * kCB)[e] = scale;
+        if constexpr (kMin) reinterpret_cast<uint16_t*>(chunk + kQ41MinOff)[e] = minv;
         uint4* c4 = reinterpret_cast<uint4*>(chunk + e * kCB);
         c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
         if constexpr (!kQ4) c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -190,15 +197,23 @@ __device__ __forceinline__ void lds_words(const uint8_t* base, int a, uint32_t* 
 //   Q6_K quant.rs:515-600: d = fp16 at 0; element i: low = nibble of byte 2 + i / 2
 //        (even i: low nibble), high = bits 2 (i % 4) of byte 66 + i / 4,
 //        q = low + 16 high - 32, scale = int8 byte 130 + i / 16.
+//   Q5_K quant.rs:433-505: d = fp16 at 0, dmin = fp16 at 2, scale of sub-block sb =
+//        byte 4 + sb & 0x3F, minimum = nibble sb % 2 of byte 12 + sb / 2 (even sb: low),
+//        element i: q4 = nibble of byte 36 + 16 sb + i / 2 (even i: high), high bit =
+//        bit i % 8 of byte 20 + sb; value (q4 + 16 bit - 16) d scale + dmin minimum.
+//        Written as a Q6_K chunk with 6-bit code q4 + 16 bit - 16 (low nibble q4, top
+//        bits 0 for bit 1, 3 for bit 0), the scale in both halves, then dmin per row
+//        and the minimum per slot.
 template <int kType>
 __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uint8_t* __restrict__ gguf,
                                                                        uint32_t src_bytes, int64_t n,
                                                                        int64_t supers, int64_t groups,
                                                                        int64_t quads,
                                                                        uint8_t* __restrict__ chunks) {
-    constexpr bool kQ6 = kType == OPENMINI_QMM_Q6_K;
-    constexpr int kBPB = kQ6 ? 210 : 144;
-    constexpr int kChunk = kQ6 ? kQ6KChunk : kQ4KChunk;
+    constexpr bool kQ5 = kType == OPENMINI_QMM_Q5_K;
+    constexpr bool kQ6 = kType == OPENMINI_QMM_Q6_K || kQ5;  // Q6_K chunk layout
+    constexpr int kBPB = kQ5 ? 176 : kType == OPENMINI_QMM_Q6_K ? 210 : 144;
+    constexpr int kChunk = kQ5 ? kQ5KChunk : kQ6 ? kQ6KChunk : kQ4KChunk;
     constexpr int kScaleOff = kQ6 ? kTileEntries * 24 : kTileEntries * 16;
     constexpr int kDOff = kScaleOff + (kQ6 ? 2 : 1) * kTileEntries;
     constexpr int kSpan = 2 * kBPB;                // one row's bytes in the workgroup
@@ -254,8 +269,8 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
     const int sub = (c & 1) * kTileBlocks + (e >> 4);  // 32-element sub-block of super-block s0 + c / 2
     uint8_t* ch = chunks + (rt * groups + g) * kChunk;
     uint32_t w[6] = {0, 0, 0, 0, 0, 0};
-    uint32_t sc = 0;
-    uint16_t dbits = 0;
+    uint32_t sc = 0, mn = 0;
+    uint16_t dbits = 0, dmbits = 0;
     if (row < n) {
         const int blk = r * kRowDw * 4 + (int)(span_off(r) & 3u) + (c >> 1) * kBPB;  // LDS byte address
         const uint16_t d = (uint16_t)(st8[blk] | (st8[blk + 1] << 8));
@@ -277,6 +292,32 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
             // dmin * 0 is NaN for an inf / NaN dmin, and so is every value of the block
             const uint16_t dmin = (uint16_t)(st8[blk + 2] | (st8[blk + 3] << 8));
             dbits = (dmin & 0x7C00u) == 0x7C00u ? (uint16_t)0x7E00u : d;
+        } else if constexpr (kQ5) {
+            lds_words<4>(st8, blk + 36 + sub * 16, qw);
+            // low nibbles, element 2 m in the HIGH nibble of s_m (as Q4_0), kept as the
+            // code's low 4 bits (no sign flip)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t pp = __builtin_amdgcn_perm(0u, qw[j], 0x01010000u);  // s0 s0 s1 s1
+                const uint32_t rr = __builtin_amdgcn_perm(0u, qw[j], 0x03030202u);  // s2 s2 s3 s3
+                const uint32_t lo = ((pp >> 4) & 0x000F000Fu) | (pp & 0x0F000F00u);
+                const uint32_t hi = (rr & 0x00F000F0u) | ((rr << 4) & 0xF000F000u);
+                w[j] = lo | hi;
+            }
+            // top bits of element 16 m + 4 f + i: 3 * (1 - bit (4 f + i) % 8 of the qh
+            // byte), the same for both words: byte i = 51 nb_i + 204 nb_(4 + i) with
+            // nb = the inverted qh bits
+            const uint32_t nb = ~(uint32_t)st8[blk + 20 + sub] & 0xFFu;
+            uint32_t top = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) top |= (51u * ((nb >> i) & 1u) + 204u * ((nb >> (4 + i)) & 1u)) << (8 * i);
+            w[4] = w[5] = top;
+            const uint32_t s6 = st8[blk + 4 + sub] & 0x3Fu;
+            sc = s6 | (s6 << 8);
+            const uint32_t mb = st8[blk + 12 + (sub >> 1)];
+            mn = (sub & 1) ? (mb >> 4) : (mb & 0x0Fu);
+            dbits = d;
+            dmbits = (uint16_t)(st8[blk + 2] | (st8[blk + 3] << 8));
         } else {
             lds_words<4>(st8, blk + 2 + sub * 16, qw);
             // low nibbles, element 2 m in the LOW nibble of s_m: chunk bytes
@@ -316,6 +357,10 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
         reinterpret_cast<uint16_t*>(ch + kScaleOff)[e] = (uint16_t)sc;
     }
     if ((e >> 4) == 0) reinterpret_cast<uint16_t*>(ch + kDOff)[r] = dbits;
+    if constexpr (kQ5) {
+        ch[kQ5KMinOff + e] = (uint8_t)mn;
+        if ((e >> 4) == 0) reinterpret_cast<uint16_t*>(ch + kQ5KDminOff)[r] = dmbits;
+    }
 }
 
 // Chunked weight -> f32 [n][k] (8 * nwords outputs, row-major; one code word = 8
@@ -677,15 +722,24 @@ hipError_t launch_repack_chunks(const Weight& w, const uint8_t* gguf, hipStream_
         if (w.type == OPENMINI_QMM_Q4_K)
             hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q4_K>, grid, dim3(kRepackThreads), 0, s, gguf,
                                (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
+        else if (w.type == OPENMINI_QMM_Q5_K)
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q5_K>, grid, dim3(kRepackThreads), 0, s, gguf,
+                               (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
         else
             hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q6_K>, grid, dim3(kRepackThreads), 0, s, gguf,
                                (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
         return hipGetLastError();
     }
-    const int aligned = ((uintptr_t)gguf % 16) == 0 && w.nb % 8 == 0;
+    // staged rows start 16-byte aligned: an aligned source and nb * bytes per block a
+    // multiple of 16 (Q4_0 / Q8_0: nb % 8 == 0, Q4_1: nb % 4 == 0)
+    const int aligned = ((uintptr_t)gguf % 16) == 0 && (w.nb * bytes_per_block(w.type)) % 16 == 0;
     const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
     constexpr int kQ4Quads = 2, kQ8Quads = 2;
-    if (w.type == OPENMINI_QMM_Q4_0) {
+    if (w.type == OPENMINI_QMM_Q4_1) {
+        const int64_t per_tile = (quads + kQ4Quads - 1) / kQ4Quads;
+        hipLaunchKernelGGL((repack_kernel<20, kQ4Quads>), dim3((unsigned)(w.n_tiles * per_tile)),
+                           dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups, per_tile, aligned, w.chunks);
+    } else if (w.type == OPENMINI_QMM_Q4_0) {
         const int64_t per_tile = (quads + kQ4Quads - 1) / kQ4Quads;
         hipLaunchKernelGGL((repack_kernel<18, kQ4Quads>), dim3((unsigned)(w.n_tiles * per_tile)),
                            dim3(kRepackThreads), 0, s, gguf, w.n, w.nb, w.groups, per_tile, aligned, w.chunks);

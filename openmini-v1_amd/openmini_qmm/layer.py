@@ -11,8 +11,8 @@ several linear layers on one input:
     itself are not part of the quantized linear layer.
 
 The host-array methods are synchronous and mirror the reference's signatures; from
-GEMM_MIN_ROWS rows on (prefill) they run the fp32-activation GEMMs, below it the
-decode GEMVs.  The *_device methods take device buffers and a stream and only enqueue
+GEMM_MIN_ROWS rows on (prefill) they run the fp32-activation GEMMs, below it (and for
+Q4_1 / Q5_K weights, whose blocks carry a minimum) the decode GEMVs.  The *_device methods take device buffers and a stream and only enqueue
 work.
 """
 from __future__ import annotations
@@ -22,7 +22,7 @@ import ctypes
 import numpy as np
 
 from ._native import check, lib
-from .ops import GEMM_MIN_ROWS, DeviceBuffer, InvalidInput, QuantizedWeight, gemm_f32_workspace
+from .ops import DeviceBuffer, InvalidInput, QuantizedWeight, gemm_f32_workspace
 
 MAX_GROUP = 4  # weights per gemv_multi launch
 
@@ -99,12 +99,19 @@ class FFNWeights:
         d_x = DeviceBuffer.from_numpy(x)
         d_h = DeviceBuffer(m * self.intermediate_size * 4)
         d_out = DeviceBuffer(m * self.down_proj.n_rows * 4)
-        if m >= GEMM_MIN_ROWS:
-            work = gemm_f32_workspace(m, max(self.hidden_size, self.intermediate_size))
-            ffn_gate_up_f32(self.gate_proj, self.up_proj, d_x, d_h, m, work)
-            self.down_proj.gemm_f32(d_h, d_out, m, work)
-        else:
+        pair_gemm, down_gemm = self.gate_proj.prefill_gemm(m), self.down_proj.prefill_gemm(m)
+        if not pair_gemm and not down_gemm:
             self.forward_device(d_x, d_h, d_out, m)
+        else:
+            work = gemm_f32_workspace(m, max(self.hidden_size, self.intermediate_size))
+            if pair_gemm:
+                ffn_gate_up_f32(self.gate_proj, self.up_proj, d_x, d_h, m, work)
+            else:
+                ffn_gate_up(self.gate_proj, self.up_proj, d_x, d_h, m)
+            if down_gemm:
+                self.down_proj.gemm_f32(d_h, d_out, m, work)
+            else:
+                self.down_proj.gemv(d_h, d_out, m)
         return d_out.download(np.float32, (m, self.down_proj.n_rows))
 
     def hidden(self, x: np.ndarray) -> np.ndarray:
@@ -113,7 +120,7 @@ class FFNWeights:
         m = x.shape[0]
         d_x = DeviceBuffer.from_numpy(x)
         d_h = DeviceBuffer(m * self.intermediate_size * 4)
-        if m >= GEMM_MIN_ROWS:
+        if self.gate_proj.prefill_gemm(m):
             ffn_gate_up_f32(self.gate_proj, self.up_proj, d_x, d_h, m, gemm_f32_workspace(m, self.hidden_size))
         else:
             ffn_gate_up(self.gate_proj, self.up_proj, d_x, d_h, m)
@@ -143,7 +150,7 @@ class AttentionWeights:
         d_x = DeviceBuffer.from_numpy(x)
         ws = (self.q_proj, self.k_proj, self.v_proj)
         outs = [DeviceBuffer(m * w.n_rows * 4) for w in ws]
-        if m >= GEMM_MIN_ROWS:
+        if self.q_proj.prefill_gemm(m):
             work = gemm_f32_workspace(m, self.q_proj.k_cols)
             for w, o in zip(ws, outs):
                 w.gemm_f32(d_x, o, m, work)
@@ -159,7 +166,7 @@ class AttentionWeights:
         m = attn.shape[0]
         d_a = DeviceBuffer.from_numpy(attn)
         d_o = DeviceBuffer(m * self.o_proj.n_rows * 4)
-        if m >= GEMM_MIN_ROWS:
+        if self.o_proj.prefill_gemm(m):
             self.o_proj.gemm_f32(d_a, d_o, m)
         else:
             self.o_proj.gemv(d_a, d_o, m)

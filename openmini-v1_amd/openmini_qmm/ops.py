@@ -28,7 +28,8 @@ QK = 32
 
 class GgufTensorType(enum.IntEnum):
     """GGUF type ids, model/inference/gguf.rs:219-240: the layouts this library
-    dequantizes (weights for the GEMV and GEMM: Q4_0, Q8_0, Q4_K and Q6_K)."""
+    dequantizes (weights for the GEMV: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K and Q6_K; for the
+    GEMM the same without Q4_1 and Q5_K)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
@@ -168,9 +169,9 @@ def init(device: int = 0) -> None:
 # ---- weights ------------------------------------------------------------------------
 
 class QuantizedWeight:
-    """A GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor W[n_rows, k_cols] uploaded and repacked in
-    HBM, served by the decode GEMV and the prefill GEMM (dequantize() takes Q4_0 and
-    Q8_0 handles).
+    """A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K tensor W[n_rows, k_cols] uploaded and
+    repacked in HBM, served by the decode GEMV and (all but Q4_1 / Q5_K, whose blocks
+    carry a minimum) the prefill GEMM; dequantize() takes Q4_0 and Q8_0 handles.
 
     Replaces QuantizedWeightLoader::load_tensor_data (quant_loader.rs:76-92), which
     dequantizes to f32 at load; here the raw blocks stay quantized on the GPU."""
@@ -213,6 +214,11 @@ class QuantizedWeight:
         self.tensor_type = GgufTensorType(int(tensor_type))
         self.n_rows, self.k_cols = int(n_rows), int(k_cols)
         return self
+
+    def prefill_gemm(self, m: int) -> bool:
+        """Whether linear() on m rows of this weight runs the fp32 prefill GEMM (the
+        library's rule: from GEMM_MIN_ROWS rows, types without a block minimum)."""
+        return m >= GEMM_MIN_ROWS and int(self.tensor_type) not in (GgufTensorType.Q4_1, GgufTensorType.Q5K)
 
     def info(self) -> _native.WeightInfo:
         info = _native.WeightInfo()
@@ -456,7 +462,7 @@ class HipQuantGemmEngine:
         dx = DeviceBuffer.from_numpy(x)
         m = x.shape[0]
         dh = DeviceBuffer(m * gate.n_rows * 4)
-        if m >= GEMM_MIN_ROWS:  # prefill: the fp32 GEMM pair on one split of x
+        if gate.prefill_gemm(m):  # prefill: the fp32 GEMM pair on one split of x
             work = gemm_f32_workspace(m, gate.k_cols)
             check(lib().openmini_qmm_ffn_gate_up_f32(gate.handle, up.handle, dx.ptr, dh.ptr, m, work.ptr,
                                                       work.nbytes, None))

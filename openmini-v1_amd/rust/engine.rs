@@ -14,13 +14,16 @@ use crate::model::inference::error::{InferenceError, InferenceResult};
 use crate::model::inference::gemm_engine::GemmBackendType;
 use crate::model::inference::gguf::GgufTensorType;
 
-/// A GGUF Q4_0 / Q8_0 / Q4_K / Q6_K tensor W[n, k] repacked in HBM; the quantized data is
-/// immutable after upload (a weight that splits K in batched calls also holds their
-/// scratch, which the library orders for the host-pointer calls this engine makes).
+/// A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K tensor W[n, k] repacked in HBM; the
+/// quantized data is immutable after upload (a weight that splits K in batched calls
+/// also holds their scratch, which the library orders for the host-pointer calls this
+/// engine makes).
 pub struct HipQuantWeight {
     pub(crate) raw: *mut ffi::QWeight,
     pub n: usize,
     pub k: usize,
+    /// GGUF type id (Q4_1 = 3 and Q5_K = 13 carry a block minimum: no prefill GEMM)
+    pub tensor_type: i32,
 }
 unsafe impl Send for HipQuantWeight {}
 unsafe impl Sync for HipQuantWeight {}
@@ -39,7 +42,13 @@ impl HipQuantWeight {
             ffi::openmini_qmm_upload(t as i32, blocks.as_ptr().cast(), blocks.len(), n_rows as i64,
                                      k_cols as i64, &mut raw)
         })?;
-        Ok(Self { raw, n: n_rows, k: k_cols })
+        Ok(Self { raw, n: n_rows, k: k_cols, tensor_type: t as i32 })
+    }
+
+    /// Whether linear() on `m` rows of this weight runs the fp32 prefill GEMM (the
+    /// library's rule: from GEMM_MIN_ROWS rows, types without a block minimum).
+    pub fn prefill_gemm(&self, m: usize) -> bool {
+        m >= GEMM_MIN_ROWS && self.tensor_type != 3 && self.tensor_type != 13
     }
 
     pub fn info(&self) -> Result<ffi::WeightInfo, String> {
@@ -161,7 +170,7 @@ impl QuantGemmEngine for HipQuantGemmEngine {
             unsafe {
                 ffi::check(ffi::openmini_qmm_memcpy_h2d(dx.0, x.as_ptr().cast(), m * k * 4, std::ptr::null_mut()))
                     .map_err(gen_err)?;
-                if m >= GEMM_MIN_ROWS {
+                if gate.prefill_gemm(m) {
                     // prefill: the fp32 GEMM pair on one split of x
                     let wb = ffi::openmini_qmm_gemm_f32_workspace_bytes(m as i64, k as i64);
                     let work = DeviceBuf::new(wb).map_err(gen_err)?;

@@ -46,7 +46,7 @@ impl HipGguf {
         ffi::check(unsafe {
             ffi::openmini_qmm_gguf_upload_weight(self.0, c.as_ptr(), std::ptr::null_mut(), &mut raw)
         })?;
-        Ok(HipQuantWeight { raw, n: info.dims[1] as usize, k: info.dims[0] as usize })
+        Ok(HipQuantWeight { raw, n: info.dims[1] as usize, k: info.dims[0] as usize, tensor_type: info.tensor_type })
     }
 
     /// get_tensor_data_by_ref (gguf.rs:2062-2110) for a non-projection tensor: f32 on the

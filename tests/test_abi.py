@@ -56,7 +56,9 @@ def test_host_only_validation():
     # too few bytes: InsufficientData{expected=36, actual=20}
     assert L.openmini_qmm_upload(2, p, 20, 1, 64, ctypes.byref(h)) == _native.ERR_INSUFFICIENT_DATA
     assert b"expected 36" in L.openmini_qmm_last_error() and b"actual 20" in L.openmini_qmm_last_error()
-    assert L.openmini_qmm_upload(3, p, 64, 1, 32, ctypes.byref(h)) == _native.ERR_UNSUPPORTED
+    # weight types: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K; Q2_K is dequantized only
+    assert L.openmini_qmm_upload(10, p, 64, 1, 256, ctypes.byref(h)) == _native.ERR_UNSUPPORTED
+    assert b"Q5_K=13" in L.openmini_qmm_last_error()
     # tiled codes must stay below 4 GiB (32-bit buffer offsets in the kernels)
     assert L.openmini_qmm_upload(7, p, 64, 1 << 19, 8192, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
     assert b"exceed 4 GiB" in L.openmini_qmm_last_error()
