@@ -178,3 +178,23 @@ def test_minfmt_ffn_forward_mixed_types(qmm, orc):
     g, u = orc.linear_f64(Q5_K, gb, I, H, x), orc.linear_f64(Q5_K, ub, I, H, x)
     h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
     assert_parity(y, orc.linear_f64(Q6_K, db, H, I, h), 2 * TOL, "mixed ffn")
+
+
+@pytest.mark.parametrize("qtype", [Q4_1, Q5_K])
+@pytest.mark.parametrize("dialect", ["reference", "standard"])
+def test_minfmt_from_gguf_file(qmm, tmp_path, qtype, dialect):
+    """A Q4_1 / Q5_K projection read from a GGUF file uploads as its raw blocks and gives
+    exactly what the same bytes give through openmini_qmm_upload."""
+    import gguf_fixtures as fx
+    from openmini_qmm import gguf as G
+    N, K = 96, 1536
+    blocks = blocks_of(qtype, N, K, 0xD900 + qtype)
+    path = tmp_path / "mf.gguf"
+    path.write_bytes(fx.build([("general.architecture", fx.STRING, "llama")],
+                              [("model.layers.0.ffn.up_proj", [K, N], qtype, blocks.tobytes())], dialect))
+    print(f"minfmt gguf type={qtype} dialect={dialect}", flush=True)
+    w_file = G.GgufFile(str(path)).upload_weight("model.layers.0.ffn.up_proj")
+    w_direct = qmm.QuantizedWeight(qtype, blocks, N, K)
+    assert w_file.info().gguf_bytes == blocks.size
+    x = synth.normal(0xD901, (5, K), 1.0)
+    assert np.array_equal(gemv_nan_filled(qmm, w_file, x), gemv_nan_filled(qmm, w_direct, x))
