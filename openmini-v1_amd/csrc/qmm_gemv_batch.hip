@@ -433,18 +433,17 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
 
     if (g0 < g1) {  // uniform per wave
         St sa, sb;
-        int g = g0;
-        load(sa, g);
-        // the loads past the slice end re-read its last group (cache hits) and are
-        // never consumed, so every path issues the same loads
-        while (true) {
+        load(sa, g0);
+        // The loads past the slice end re-read its last group (cache hits) and are
+        // never consumed, so every path issues the same loads.  One exit, at the loop
+        // test: with a break between the two halves the compiler's wait insertion
+        // merged the paths conservatively and waited at the loop head for the
+        // prefetched stage to land before issuing the next one.
+        for (int g = g0; g < g1; g += 2) {
             load(sb, min(g + 1, g1 - 1));
             compute(sa);
-            if (g + 1 >= g1) break;
             load(sa, min(g + 2, g1 - 1));
-            compute(sb);
-            if (g + 2 >= g1) break;
-            g += 2;
+            if (g + 1 < g1) compute(sb);
         }
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the unconsumed prefetch has landed
     }
