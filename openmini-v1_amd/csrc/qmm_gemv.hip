@@ -359,7 +359,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                     b1 = i32x4{(int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
                 }
                 // the slot's fp32 factor(s), exact: fp16 scale; Q4_K d * scale; Q6_K d * scale
-                // of each 16-element half.  Groups past the slice end get 0.
+                // of each 16-element half; Q5_K d * scale (its two scale bytes are equal).
+                // Groups past the slice end get 0.
                 const bool live = g + p < g1;
                 float d0, d1 = 0.0f;
                 if constexpr (kFmt == OPENMINI_QMM_Q4_K) {
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                     const i32x4 A0 = i32x4{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w};
                     const i32x4 A1 = i32x4{(int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
                     const int sh = -shift[p][b] - F::kCodeShift;
-                    if constexpr (F::kQ6) {
+                    if constexpr (F::kQ6 && !F::kQ5) {
                         // the halves carry different scales: one MFMA each, not chained
                         const i32x4 D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, i32x4{0, 0, 0, 0}, 0, 0, 0);
                         const i32x4 D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, i32x4{0, 0, 0, 0}, 0, 0, 0);

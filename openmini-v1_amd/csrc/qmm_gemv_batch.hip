@@ -17,6 +17,8 @@
 //     their 32-element sub-blocks as the blocks, with block factor d * scale (exact).
 //     Q6_K's scale changes every 16 elements, inside one MFMA's 32: each half runs its
 //     own MFMA pair with the other half's codes zeroed, scaled by its own factor.
+//     Q5_K shares Q6_K's chunk layout but has one scale per 32 elements: one MFMA
+//     pair per block, like Q4_K.
 //   * Per (batch row, 4-block group) the activations are scaled by 2^s, s chosen so
 //     the group's largest |x| lands in [2^14, 2^15), and split into hi = x' rounded
 //     toward zero to fp16 (11 significant bits: x' with its low 13 mantissa bits
@@ -373,14 +375,15 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                 transpose4(o[0], o[1], o[2], o[3]);
             }
             // the block factors of column i (slot (t, i) for t = 0..3), exact in fp32:
-            // the fp16 scale; Q4_K d * scale; Q6_K d * scale of each 16-element half
+            // the fp16 scale; Q4_K d * scale; Q6_K d * scale of each 16-element half;
+            // Q5_K d * scale (one per 32-element sub-block: its two scale bytes are equal)
             float ds[4], ds1[4];
             if constexpr (F::kQ4K) {
                 broadcast4(f16_bits_to_f32((uint16_t)st.dk[i]) * (float)(st.sc[i] & 0xFFu), ds);
             } else if constexpr (F::kQ6K) {
                 const float dd = f16_bits_to_f32((uint16_t)st.dk[i]);
                 broadcast4(dd * (float)(int8_t)(st.sc[i] & 0xFFu), ds);
-                broadcast4(dd * (float)(int8_t)((st.sc[i] >> 8) & 0xFFu), ds1);
+                if constexpr (!F::kQ5) broadcast4(dd * (float)(int8_t)((st.sc[i] >> 8) & 0xFFu), ds1);
             } else {
                 broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
             }
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                     b = codes_q6(e[t], o[t], kq);
                 else
                     b = codes_q8(e[t], o[t]);
-                if constexpr (F::kQ6K) {
+                if constexpr (F::kQ6K && !F::kQ5) {
                     // the halves carry their own factors: lanes kq = 0, 1 hold the
                     // block's elements 0..15, lanes 2, 3 elements 16..31; one MFMA pair
                     // per half with the other half's codes zeroed
