@@ -452,8 +452,11 @@ hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, 
 }
 
 // K slices per row tile (phases of 4 groups).  One batch row: W = 8 or 16, whichever
-// pads the last phases with fewer groups (ties: 16, more waves); measured on MI355X,
-// e.g. K = 4096 -> 8, 8192 -> 16, 11008 -> 8.  Nibble codes on at most 512 row tiles
+// pads the last phases with fewer groups; ties (K a multiple of 8192): 8, two phases
+// per wave and twice the resident workgroups per CU (three interleaved passes, one
+// box, 28672 x 8192: Q8_0 44.1-44.3 -> 41.9 us, also over 500 launches 43.8 -> 41.6;
+// Q4_0 25.4-25.5 -> 24.4-24.6 us, over 500 launches even at 22.5-22.8; Q4_K 25.2-25.4
+// -> 24.4-24.5 us).  E.g. K = 4096 -> 8, 11008 -> 8.  Nibble codes on at most 512 row tiles
 // (two workgroups per CU or fewer) with K of 64+ groups: 16 waves of 2-group phases,
 // twice the waves in flight (two interleaved passes, Q4_0: 4096 x 11008 7.25-7.58 ->
 // 7.03-7.14 us, 8192 x 28672 26.7-27.3 -> 25.5-25.6, 8192 x 8192 8.40-8.51 ->
@@ -469,7 +472,7 @@ hipError_t run_w(const GemvGroup& grp, int64_t g, int64_t k, const float* x, hip
             if (g >= 64 && grp.tile_begin[kMaxGroup] <= 512) return run<kFmt, B, 16, 2, kKind>(grp, g, k, x, s);
         if constexpr (B == 1) {
             const int64_t pad16 = (g + 63) / 64 * 64 - g, pad8 = (g + 31) / 32 * 32 - g;
-            if (pad16 <= pad8) return run<kFmt, B, 16, 4, kKind>(grp, g, k, x, s);
+            if (pad16 < pad8) return run<kFmt, B, 16, 4, kKind>(grp, g, k, x, s);
         }
         return run<kFmt, B, 8, 4, kKind>(grp, g, k, x, s);
     }
