@@ -57,9 +57,9 @@ typedef enum {
 } openmini_qmm_status_t;
 
 /* GGUF tensor type ids (src/model/inference/gguf.rs:219-240).  Weight upload and the
- * decode GEMV take Q4_0, Q4_1, Q8_0, Q4_K, Q5_K and Q6_K; the prefill GEMM the same
- * without Q4_1 and Q5_K (their blocks carry a minimum); the dequantization entry points
- * take every id listed. */
+ * decode GEMV take Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K and Q8_K; the prefill GEMM the
+ * same without Q4_1 and Q5_K (their blocks carry a minimum); the dequantization entry
+ * points take every id listed. */
 typedef enum {
     OPENMINI_QMM_F32 = 0,
     OPENMINI_QMM_F16 = 1,
@@ -81,9 +81,9 @@ typedef struct {
     int32_t type;            /* openmini_qmm_type_t */
     int32_t device;          /* HIP device ordinal holding the weight */
     int64_t n_rows;          /* N: output features */
-    int64_t k_cols;          /* K: input features, a multiple of 32 (256 for Q4_K / Q5_K / Q6_K) */
+    int64_t k_cols;          /* K: input features, a multiple of 32 (256 for Q4_K / Q5_K / Q6_K / Q8_K) */
     int64_t blocks_per_row;  /* K / 32 (32-element sub-blocks for the K-quants) */
-    size_t gguf_bytes;       /* GGUF data_size: N * K / 32 * 18 | 34, N * K / 256 * 144 | 210 */
+    size_t gguf_bytes;       /* GGUF data_size: N * K / 32 * 18 | 20 | 34, N * K / 256 * 144 | 176 | 210 | 258 */
     size_t device_bytes;     /* HBM held by the handle */
 } openmini_qmm_weight_info_t;
 
@@ -138,8 +138,10 @@ size_t openmini_qmm_estimate_memory_usage(int type, size_t n_elements);
  * products of an integer code and an fp32 sub-block factor); Q4_1 and Q5_K (GEMV only:
  * q * d + m, quant.rs:216-262, and the reference's Q5_K reading (q - 16) * d * scale +
  * dmin * minimum, quant.rs:433-505; each block's product gains its minimum times the
- * block's activation sum).
- * Errors: INVALID_PARAM (k_cols % 32, or % 256 for the K-quants; sizes <= 0),
+ * block's activation sum); Q8_K (the reference's 258-byte reading, fp16 d and 256
+ * int8 codes, value q * d, quant.rs:768-800: eight Q8_0 blocks sharing d, stored and
+ * served as Q8_0 with the same values).
+ * Errors: INVALID_PARAM (k_cols % 32, or % 256 for the K-quants and Q8_K; sizes <= 0),
  * UNSUPPORTED (type), INSUFFICIENT_DATA (gguf_bytes < required). */
 int openmini_qmm_upload(int type, const void* gguf_blocks, size_t gguf_bytes,
                         int64_t n_rows, int64_t k_cols, openmini_qweight_t** out_weight);
@@ -283,7 +285,7 @@ int openmini_qmm_linear_host_noalloc(const openmini_qweight_t* weight, const flo
 
 /* ---- dequantization (GpuQuantOps, src/model/inference/quant_simd.rs:2944-2986) ----- */
 
-/* Dequantizes an uploaded Q4_0 / Q8_0 weight to f32 W[N, K] (row-major) in device memory
+/* Dequantizes an uploaded Q4_0 / Q8_0 / Q8_K weight to f32 W[N, K] (row-major) in device memory
  * (d_out 16-byte aligned).  Bit-identical to quant::dequantize of the original GGUF bytes.
  * UNSUPPORTED for the other weight types: their GGUF bytes dequantize through
  * openmini_qmm_dequantize_any_device. */

@@ -73,10 +73,11 @@ int hip_fail(hipError_t e, const char* what) {
     } while (0)
 
 // Weight layouts of the upload and the decode GEMV; the prefill GEMM takes those
-// without a block minimum (not Q4_1 / Q5_K), dequant_weight Q4_0 and Q8_0.
+// without a block minimum (not Q4_1 / Q5_K), dequant_weight Q4_0 and Q8_0 (Q8_K
+// weights are stored as Q8_0 chunks: chunk_type).
 bool type_supported(int type) {
     return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_1 || type == OPENMINI_QMM_Q8_0 ||
-           qmm::is_kquant(type);
+           qmm::is_kquant(type) || type == OPENMINI_QMM_Q8_K;
 }
 int check_gemm_type(const qmm::Weight& w) {
     if (qmm::has_block_min(w.type))
@@ -138,7 +139,8 @@ size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_cols) {
     if (!type_supported(type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
-                    "unsupported tensor type %d (Q4_0=2, Q4_1=3, Q8_0=7, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+                    "unsupported tensor type %d (Q4_0=2, Q4_1=3, Q8_0=7, Q4_K=12, Q5_K=13, Q6_K=14, Q8_K=15)",
+                    type);
     if (n_rows <= 0 || k_cols <= 0)
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "invalid shape [%lld, %lld]", (long long)n_rows,
                     (long long)k_cols);
@@ -153,7 +155,7 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
     // largest Llama-70B projection is 0.23 G).
     const size_t chunked = (size_t)((n_rows + qmm::kTileRows - 1) / qmm::kTileRows) *
                            (size_t)((k_cols / qmm::kQK + qmm::kTileBlocks - 1) / qmm::kTileBlocks) *
-                           (size_t)qmm::chunk_bytes(type);
+                           (size_t)qmm::chunk_bytes(qmm::chunk_type(type));
     if (chunked >= ((size_t)1 << 32))
         return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "shape [%lld, %lld]: %zu weight bytes exceed 4 GiB",
                     (long long)n_rows, (long long)k_cols, chunked);
@@ -166,15 +168,16 @@ int validate_weight_args(int type, size_t gguf_bytes, int64_t n_rows, int64_t k_
 
 // The weight's geometry and device size (chunks, then the K-split workspace).
 void plan_weight(int type, int64_t n_rows, int64_t k_cols, int dev, qmm::Weight& w) {
-    w.type = type;
+    w.src_type = type;
+    w.type = qmm::chunk_type(type);
     w.device = dev;
     w.n = n_rows;
     w.k = k_cols;
     w.nb = k_cols / qmm::kQK;
     w.n_tiles = (w.n + qmm::kTileRows - 1) / qmm::kTileRows;
     w.groups = (w.nb + qmm::kTileBlocks - 1) / qmm::kTileBlocks;
-    w.chunk_bytes = (size_t)qmm::chunk_bytes(type);
-    qmm::batch_split(type, w.n_tiles, w.groups, &w.split_t, &w.split_s);
+    w.chunk_bytes = (size_t)qmm::chunk_bytes(w.type);
+    qmm::batch_split(w.type, w.n_tiles, w.groups, &w.split_t, &w.split_s);
     w.device_bytes = round_up((size_t)w.n_chunks() * w.chunk_bytes, 256) +
                      qmm::split_workspace_bytes(w.n_tiles, w.split_t, w.split_s);
 }
@@ -476,12 +479,13 @@ void openmini_qmm_free_weight(openmini_qweight_t* weight) {
 int openmini_qmm_weight_info(const openmini_qweight_t* weight, openmini_qmm_weight_info_t* info) {
     if (!weight || !info) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "null argument");
     const qmm::Weight& w = weight->w;
-    info->type = w.type;
+    info->type = w.src_type;
     info->device = w.device;
     info->n_rows = w.n;
     info->k_cols = w.k;
     info->blocks_per_row = w.nb;
-    info->gguf_bytes = (size_t)w.n * (size_t)(w.k / qmm::weight_block_elems(w.type)) * qmm::bytes_per_block(w.type);
+    info->gguf_bytes =
+        (size_t)w.n * (size_t)(w.k / qmm::weight_block_elems(w.src_type)) * qmm::bytes_per_block(w.src_type);
     info->device_bytes = w.device_bytes;
     return ok();
 }
@@ -731,7 +735,7 @@ int openmini_qmm_dequant_weight(const openmini_qweight_t* weight, float* d_out, 
     if (!aligned16(d_out)) return fail(OPENMINI_QMM_ERR_INVALID_PARAM, "out must be 16-byte aligned");
     if (!plain_type(weight->w.type))
         return fail(OPENMINI_QMM_ERR_UNSUPPORTED,
-                    "dequant_weight takes Q4_0 and Q8_0 weights (K-quant bytes: openmini_qmm_dequantize_any_device)");
+                    "dequant_weight takes Q4_0, Q8_0 and Q8_K weights (K-quant bytes: openmini_qmm_dequantize_any_device)");
     hipError_t e = qmm::launch_dequant_weight(weight->w, d_out, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "dequant launch");
     return ok();

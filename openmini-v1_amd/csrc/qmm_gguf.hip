@@ -581,10 +581,10 @@ int openmini_qmm_gguf_upload_weight(const openmini_qmm_gguf_t* g, const char* na
         return gfail(OPENMINI_QMM_ERR_INVALID_PARAM, "%s has %zu dimensions; a linear weight has 2 ([K, N])",
                      name, t->dims.size());
     if (t->type != OPENMINI_QMM_Q4_0 && t->type != OPENMINI_QMM_Q4_1 && t->type != OPENMINI_QMM_Q8_0 &&
-        !qmm::is_kquant(t->type))
+        !qmm::is_kquant(t->type) && t->type != OPENMINI_QMM_Q8_K)
         return gfail(OPENMINI_QMM_ERR_UNSUPPORTED,
-                     "%s is tensor type %d; weights upload as Q4_0 (2), Q4_1 (3), Q8_0 (7), Q4_K (12), Q5_K (13) or "
-                     "Q6_K (14)", name, t->type);
+                     "%s is tensor type %d; weights upload as Q4_0 (2), Q4_1 (3), Q8_0 (7), Q4_K (12), Q5_K (13), "
+                     "Q6_K (14) or Q8_K (15)", name, t->type);
     if (!fits(*g, *t)) return gfail(OPENMINI_QMM_ERR_MODEL_LOAD, "Tensor data out of bounds");
     // GGUF dims [ne0, ne1] = [K, N]: row n of W is ne0 = K consecutive elements.
     const int64_t k = (int64_t)t->dims[0], n = (int64_t)t->dims[1];

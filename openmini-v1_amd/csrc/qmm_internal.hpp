@@ -99,7 +99,7 @@ inline bool is_kquant(int type) {
     return type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q5_K || type == OPENMINI_QMM_Q6_K;
 }
 inline bool has_block_min(int type) { return type == OPENMINI_QMM_Q4_1 || type == OPENMINI_QMM_Q5_K; }
-inline int weight_block_elems(int type) { return is_kquant(type) ? 256 : 32; }
+inline int weight_block_elems(int type) { return is_kquant(type) || type == OPENMINI_QMM_Q8_K ? 256 : 32; }
 inline int bytes_per_block(int type) {
     switch (type) {
     case OPENMINI_QMM_Q4_0: return 18;
@@ -108,9 +108,15 @@ inline int bytes_per_block(int type) {
     case OPENMINI_QMM_Q4_K: return 144;
     case OPENMINI_QMM_Q5_K: return 176;
     case OPENMINI_QMM_Q6_K: return 210;
+    case OPENMINI_QMM_Q8_K: return 258;
     default: return 0;
     }
 }
+// The chunk format a weight type is stored and computed in.  The reference reads a
+// Q8_K super-block as fp16 d and 256 int8 codes, value q * d (quant.rs:768-800): eight
+// Q8_0 blocks that share one d, so Q8_K weights become Q8_0 chunks and run every Q8_0
+// kernel with the same values.
+inline int chunk_type(int type) { return type == OPENMINI_QMM_Q8_K ? OPENMINI_QMM_Q8_0 : type; }
 
 // GgufTensorType::{block_size, bytes_per_block} (src/model/inference/gguf.rs:348-379)
 // for the layouts the dequantization entry points accept; 0 for others.
@@ -174,7 +180,8 @@ __host__ __device__ __forceinline__ int slot_of(int64_t row, int64_t blk) {
 }
 
 struct Weight {
-    int type = 0;
+    int type = 0;      // chunk format (chunk_type of src_type): what the kernels dispatch on
+    int src_type = 0;  // the GGUF block type uploaded
     int device = 0;
     int64_t n = 0;        // rows
     int64_t k = 0;        // columns

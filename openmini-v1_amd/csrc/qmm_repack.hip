@@ -204,6 +204,9 @@ __device__ __forceinline__ void lds_words(const uint8_t* base, int a, uint32_t* 
 //        Written as a Q6_K chunk with 6-bit code q4 + 16 bit - 16 (low nibble q4, top
 //        bits 0 for bit 1, 3 for bit 0), the scale in both halves, then dmin per row
 //        and the minimum per slot.
+//   Q8_K quant.rs:768-800: d = fp16 at 0, element i = int8 byte 2 + i, value q d.
+//        Written as a Q8_0 chunk: the codes of 32-element sub-block sb as they stand,
+//        d as every slot's scale.
 template <int kType>
 __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uint8_t* __restrict__ gguf,
                                                                        uint32_t src_bytes, int64_t n,
@@ -212,8 +215,9 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
                                                                        uint8_t* __restrict__ chunks) {
     constexpr bool kQ5 = kType == OPENMINI_QMM_Q5_K;
     constexpr bool kQ6 = kType == OPENMINI_QMM_Q6_K || kQ5;  // Q6_K chunk layout
-    constexpr int kBPB = kQ5 ? 176 : kType == OPENMINI_QMM_Q6_K ? 210 : 144;
-    constexpr int kChunk = kQ5 ? kQ5KChunk : kQ6 ? kQ6KChunk : kQ4KChunk;
+    constexpr bool kQ8K = kType == OPENMINI_QMM_Q8_K;        // Q8_0 chunk layout
+    constexpr int kBPB = kQ8K ? 258 : kQ5 ? 176 : kType == OPENMINI_QMM_Q6_K ? 210 : 144;
+    constexpr int kChunk = kQ8K ? chunk_bytes_for(false) : kQ5 ? kQ5KChunk : kQ6 ? kQ6KChunk : kQ4KChunk;
     constexpr int kScaleOff = kQ6 ? kTileEntries * 24 : kTileEntries * 16;
     constexpr int kDOff = kScaleOff + (kQ6 ? 2 : 1) * kTileEntries;
     constexpr int kSpan = 2 * kBPB;                // one row's bytes in the workgroup
@@ -268,14 +272,17 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
     const int64_t row = row0 + r;
     const int sub = (c & 1) * kTileBlocks + (e >> 4);  // 32-element sub-block of super-block s0 + c / 2
     uint8_t* ch = chunks + (rt * groups + g) * kChunk;
-    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t sc = 0, mn = 0;
     uint16_t dbits = 0, dmbits = 0;
     if (row < n) {
         const int blk = r * kRowDw * 4 + (int)(span_off(r) & 3u) + (c >> 1) * kBPB;  // LDS byte address
         const uint16_t d = (uint16_t)(st8[blk] | (st8[blk + 1] << 8));
         uint32_t qw[4];
-        if constexpr (!kQ6) {
+        if constexpr (kQ8K) {
+            lds_words<8>(st8, blk + 2 + sub * 32, w);
+            dbits = d;
+        } else if constexpr (!kQ6) {
             lds_words<4>(st8, blk + 12 + sub * 16, qw);
             // code word j: elements 8 j .. 8 j + 7 from GGUF bytes s0..s3 (element 2 m in
             // the high nibble of s_m): chunk bytes (s0.hi | s2.hi << 4, s0.lo | s2.lo << 4,
@@ -348,7 +355,13 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
             dbits = d;
         }
     }
-    if constexpr (!kQ6) {
+    if constexpr (kQ8K) {
+        uint4* c4 = reinterpret_cast<uint4*>(ch + e * 32);
+        c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        reinterpret_cast<uint16_t*>(ch + kTileEntries * 32)[e] = dbits;
+        return;
+    } else if constexpr (!kQ6) {
         reinterpret_cast<uint4*>(ch)[e] = make_uint4(w[0], w[1], w[2], w[3]);
         ch[kScaleOff + e] = (uint8_t)sc;
     } else {
@@ -712,17 +725,20 @@ namespace {
 
 hipError_t launch_repack_chunks(const Weight& w, const uint8_t* gguf, hipStream_t s) {
     if (w.n_tiles <= 0 || w.groups <= 0) return hipSuccess;
-    if (is_kquant(w.type)) {
+    if (is_kquant(w.src_type) || w.src_type == OPENMINI_QMM_Q8_K) {
         const int64_t supers = w.k / 256;
-        const int64_t src = w.n * supers * bytes_per_block(w.type);
+        const int64_t src = w.n * supers * bytes_per_block(w.src_type);
         // 32-bit buffer offsets: the source is smaller than the chunk array (< 4 GiB)
         if (src + 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;
         const int64_t quads = (w.groups + kRepackChunks - 1) / kRepackChunks;
         const dim3 grid((unsigned)(w.n_tiles * quads));
-        if (w.type == OPENMINI_QMM_Q4_K)
+        if (w.src_type == OPENMINI_QMM_Q4_K)
             hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q4_K>, grid, dim3(kRepackThreads), 0, s, gguf,
                                (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
-        else if (w.type == OPENMINI_QMM_Q5_K)
+        else if (w.src_type == OPENMINI_QMM_Q8_K)
+            hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q8_K>, grid, dim3(kRepackThreads), 0, s, gguf,
+                               (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
+        else if (w.src_type == OPENMINI_QMM_Q5_K)
             hipLaunchKernelGGL(repack_kquant_kernel<OPENMINI_QMM_Q5_K>, grid, dim3(kRepackThreads), 0, s, gguf,
                                (uint32_t)src, w.n, supers, w.groups, quads, w.chunks);
         else

@@ -28,8 +28,8 @@ QK = 32
 
 class GgufTensorType(enum.IntEnum):
     """GGUF type ids, model/inference/gguf.rs:219-240: the layouts this library
-    dequantizes (weights for the GEMV: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K and Q6_K; for the
-    GEMM the same without Q4_1 and Q5_K)."""
+    dequantizes (weights for the GEMV: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K and Q8_K; for
+    the GEMM the same without Q4_1 and Q5_K)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
@@ -169,9 +169,10 @@ def init(device: int = 0) -> None:
 # ---- weights ------------------------------------------------------------------------
 
 class QuantizedWeight:
-    """A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K tensor W[n_rows, k_cols] uploaded and
-    repacked in HBM, served by the decode GEMV and (all but Q4_1 / Q5_K, whose blocks
-    carry a minimum) the prefill GEMM; dequantize() takes Q4_0 and Q8_0 handles.
+    """A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K / Q8_K tensor W[n_rows, k_cols]
+    uploaded and repacked in HBM, served by the decode GEMV and (all but Q4_1 / Q5_K,
+    whose blocks carry a minimum) the prefill GEMM; dequantize() takes Q4_0 and Q8_0
+    handles, and Q8_K ones (stored as the Q8_0 blocks of the same values).
 
     Replaces QuantizedWeightLoader::load_tensor_data (quant_loader.rs:76-92), which
     dequantizes to f32 at load; here the raw blocks stay quantized on the GPU."""

@@ -102,20 +102,20 @@ def weight_blocks(qtype: int, n_rows: int, k_cols: int, seed: int, sigma: float 
     return quantize(qtype, normal(seed, (n_rows, k_cols), sigma))
 
 
-Q4_K, Q5_K, Q6_K = 12, 13, 14
+Q4_K, Q5_K, Q6_K, Q8_K = 12, 13, 14, 15
 
 
 def kquant_blocks(qtype: int, n_rows: int, k_cols: int, seed: int) -> np.ndarray:
-    """Random GGUF Q4_K (144 B) / Q5_K (176 B) / Q6_K (210 B) super-blocks of W[n_rows,
-    k_cols], row n = k_cols / 256 super-blocks, with finite fp16 d (and dmin) of
-    weight-like size (values up to ~0.05).  The reference has no K-quant quantizer;
-    these blocks exercise its reading of the layouts (quant.rs:338-410, 433-505,
-    515-600): every code, scale and minimum byte is random, d and dmin are drawn small
-    and positive or negative."""
+    """Random GGUF Q4_K (144 B) / Q5_K (176 B) / Q6_K (210 B) / Q8_K (258 B) super-blocks
+    of W[n_rows, k_cols], row n = k_cols / 256 super-blocks, with finite fp16 d (and
+    dmin) of weight-like size (values up to ~0.05).  The reference has no K-quant
+    quantizer; these blocks exercise its reading of the layouts (quant.rs:338-410,
+    433-505, 515-600, 768-800): every code, scale and minimum byte is random, d and dmin
+    are drawn small and positive or negative."""
     assert k_cols % 256 == 0
     rng = np.random.default_rng(seed)
     nblk = n_rows * (k_cols // 256)
-    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210}[qtype]
+    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 258}[qtype]
     raw = rng.integers(0, 256, size=(nblk, bpb), dtype=np.uint8)
     sign = np.where(rng.random(nblk) < 0.5, -1.0, 1.0)
     if qtype == Q5_K:
@@ -128,6 +128,9 @@ def kquant_blocks(qtype: int, n_rows: int, k_cols: int, seed: int) -> np.ndarray
         dmin = (rng.standard_normal(nblk) * 1e-3).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
         raw[:, 2:4] = dmin.view(np.uint8).reshape(-1, 2)
+    elif qtype == Q8_K:
+        d = (sign * (rng.random(nblk) * 3e-4 + 1e-4)).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
     else:
         d = (sign * (rng.random(nblk) * 2e-5 + 5e-6)).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)

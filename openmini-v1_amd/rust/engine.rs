@@ -14,7 +14,7 @@ use crate::model::inference::error::{InferenceError, InferenceResult};
 use crate::model::inference::gemm_engine::GemmBackendType;
 use crate::model::inference::gguf::GgufTensorType;
 
-/// A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K tensor W[n, k] repacked in HBM; the
+/// A GGUF Q4_0 / Q4_1 / Q8_0 / Q4_K / Q5_K / Q6_K / Q8_K tensor W[n, k] repacked in HBM; the
 /// quantized data is immutable after upload (a weight that splits K in batched calls
 /// also holds their scratch, which the library orders for the host-pointer calls this
 /// engine makes).

@@ -56,9 +56,14 @@ def test_host_only_validation():
     # too few bytes: InsufficientData{expected=36, actual=20}
     assert L.openmini_qmm_upload(2, p, 20, 1, 64, ctypes.byref(h)) == _native.ERR_INSUFFICIENT_DATA
     assert b"expected 36" in L.openmini_qmm_last_error() and b"actual 20" in L.openmini_qmm_last_error()
-    # weight types: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K; Q2_K is dequantized only
+    # weight types: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K; Q2_K is dequantized only
     assert L.openmini_qmm_upload(10, p, 64, 1, 256, ctypes.byref(h)) == _native.ERR_UNSUPPORTED
-    assert b"Q5_K=13" in L.openmini_qmm_last_error()
+    assert b"Q5_K=13" in L.openmini_qmm_last_error() and b"Q8_K=15" in L.openmini_qmm_last_error()
+    # Q8_K: 256-element super-blocks of 258 bytes
+    assert L.openmini_qmm_upload(15, p, 64, 1, 288, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
+    assert b"multiple of 256" in L.openmini_qmm_last_error()
+    assert L.openmini_qmm_upload(15, p, 64, 2, 512, ctypes.byref(h)) == _native.ERR_INSUFFICIENT_DATA
+    assert b"expected 1032" in L.openmini_qmm_last_error()
     # tiled codes must stay below 4 GiB (32-bit buffer offsets in the kernels)
     assert L.openmini_qmm_upload(7, p, 64, 1 << 19, 8192, ctypes.byref(h)) == _native.ERR_INVALID_PARAM
     assert b"exceed 4 GiB" in L.openmini_qmm_last_error()
@@ -89,6 +94,15 @@ def test_host_only_validation():
     assert L.openmini_qmm_gemm_ceiling(12, 512, 11008, 4096, p, None) == _native.ERR_UNSUPPORTED
     assert L.openmini_qmm_gemm_ceiling(7, 512, 11008, 4100, p, None) == _native.ERR_INVALID_PARAM
     assert L.openmini_qmm_gemm_ceiling(7, 0, 11008, 4096, p, None) == _native.ERR_INVALID_PARAM
+
+
+def test_q8k_weights_take_q8_0_chunks():
+    """A Q8_K super-block is read as fp16 d and 256 int8 codes, value q * d
+    (quant.rs:768-800): eight Q8_0 blocks sharing d, so a Q8_K weight is stored as Q8_0
+    chunks and occupies what the Q8_0 weight of its shape does."""
+    from openmini_qmm import weight_device_bytes
+    for n, k in ((1, 256), (37, 2304), (11008, 4096), (4096, 11008), (8192, 28672)):
+        assert weight_device_bytes(15, n, k) == weight_device_bytes(7, n, k), (n, k)
 
 
 def test_python_mirror_raises_reference_errors():
