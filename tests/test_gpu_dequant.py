@@ -213,19 +213,21 @@ def test_upload_from_device_any_alignment(qmm, orc, qtype, offset):
 
 
 def test_upload_device_into_one_arena(qmm, orc):
-    """openmini_qmm_upload_device_into: three weights (Q4_0, a Q8_0 with a K-split
-    workspace, a Q4_K) placed back to back in one caller allocation at 256-byte
-    boundaries.  Each dequantizes bit-exactly, and its GEMV at 1 and 8 rows equals the
-    same weight uploaded with its own allocation, bit for bit.  Closing the handles
+    """openmini_qmm_upload_device_into: four weights (Q4_0, a Q8_0 with a K-split
+    workspace, a Q4_K, a Q8_K with a K-split workspace) placed back to back in one
+    caller allocation at 256-byte boundaries.  Each dequantizes bit-exactly (the Q4_K
+    aside), and its GEMV at 1 and 8 rows equals the same weight uploaded with its own
+    allocation, bit for bit.  Closing the handles
     leaves the arena to the caller, which then reuses it for another weight."""
-    specs = [(Q4_0, 1000, 4096, 0xD00), (Q8_0, 4096, 11008, 0xD01), (12, 777, 2048, 0xD02)]
+    specs = [(Q4_0, 1000, 4096, 0xD00), (Q8_0, 4096, 11008, 0xD01), (12, 777, 2048, 0xD02),
+             (15, 4096, 11008, 0xD03)]
     sizes = [qmm.weight_device_bytes(t, n, k) for t, n, k, _ in specs]
     offsets = np.cumsum([0] + [(b + 255) // 256 * 256 for b in sizes])
     arena = qmm.DeviceBuffer(int(offsets[-1]))
     arena.fill(0xA5)  # stale bytes: the repack and the split-counter clear must cover them
     own, placed = [], []
     for (t, n, k, seed), off, size in zip(specs, offsets, sizes):
-        blocks = synth.kquant_blocks(t, n, k, seed=seed) if t == 12 else synth.weight_blocks(t, n, k, seed=seed)
+        blocks = synth.kquant_blocks(t, n, k, seed=seed) if t >= 12 else synth.weight_blocks(t, n, k, seed=seed)
         d = qmm.DeviceBuffer.from_numpy(blocks)
         w = qmm.QuantizedWeight.from_device_into(t, d, blocks.size, n, k, arena, int(off))
         ref = qmm.QuantizedWeight(t, blocks, n, k)
