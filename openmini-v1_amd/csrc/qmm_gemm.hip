@@ -269,10 +269,14 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     };
 
     f32x4 acc[kMI][kWT];
+    // Q6_K on bf16 x: the sums of the current super-block, before its d (one per tile
+    // row and super-block); the other instances leave them unused.
+    constexpr bool kChain = F::kQ6K && !kX2;
+    f32x4 sacc[kMI][kWT];
 #pragma unroll
     for (int i = 0; i < kMI; ++i)
 #pragma unroll
-        for (int j = 0; j < kWT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kWT; ++j) acc[i][j] = sacc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // A fragments of 32-element segment tt of the step in LDS stage `stage`: rows
     // i * 16 + li, elements 8 kq .. 8 kq + 7 of the segment (swizzled); bf16 x, or the
@@ -289,31 +293,39 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     auto bf = [](const uint4& v) { return __builtin_bit_cast(bf16x8, v); };
     auto hf = [](const uint4& v) { return __builtin_bit_cast(f16x8, v); };
     // Q6_K block tt: the scale changes every 16 elements, inside an MFMA's 32, so it is
-    // folded into the codes: q * sc (exact integers) as bf16 hi + lo, two chained MFMAs
-    // per subtile, then one FMA per output with the row's d.
+    // folded into the codes: q * sc (exact integers) as bf16 hi + lo.  The d is one per
+    // tile row and super-block, so the blocks of a super-block chain into one sum per
+    // output (sacc; all hi MFMAs, then all lo ones, so no MFMA waits on the one before),
+    // and flush_q6 applies d once per super-block: one FMA per output per 8 blocks
+    // instead of one per block.
     auto compute_q6 = [&](const BRegs<kFmt, kWB, kWT>& B, const AFrags& a, int tt) {
         if constexpr (F::kQ6K && !kX2) {
             bf16x8 bh[kWT], bl[kWT];
-            float d[kWT];
+#pragma unroll
+            for (int j = 0; j < kWT; ++j)
+                split_q6(B.c[j][tt][0], B.c[j][tt][1], kq, (float)(int8_t)(B.s[j][tt] & 0xFFu) * 0.25f, bh[j], bl[j]);
+#pragma unroll
+            for (int q = 0; q < kMI * kWT; ++q)
+                sacc[q / kWT][q % kWT] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[q / kWT]), bh[q % kWT], sacc[q / kWT][q % kWT], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kMI * kWT; ++q)
+                sacc[q / kWT][q % kWT] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[q / kWT]), bl[q % kWT], sacc[q / kWT][q % kWT], 0, 0, 0);
+        }
+    };
+    // Q6_K: after the last block of a super-block, or of this K part, acc += sacc * d.
+    auto flush_q6 = [&](const BRegs<kFmt, kWB, kWT>& B) {
+        if constexpr (kChain) {
 #pragma unroll
             for (int j = 0; j < kWT; ++j) {
-                split_q6(B.c[j][tt][0], B.c[j][tt][1], kq, (float)(int8_t)(B.s[j][tt] & 0xFFu) * 0.25f, bh[j], bl[j]);
-                d[j] = f16_bits_to_f32((uint16_t)B.d[j]);
-            }
-            f32x4 pp[2];
-            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[0]), bh[0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            pp[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[0]), bl[0], pp[0], 0, 0, 0);
+                const float d = f16_bits_to_f32((uint16_t)B.d[j]);
 #pragma unroll
-            for (int q = 0; q < kMI * kWT; ++q) {
-                if (q + 1 < kMI * kWT) {
-                    const int i1 = (q + 1) / kWT, j1 = (q + 1) % kWT;
-                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[i1]), bh[j1],
-                                                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    pp[(q + 1) & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf(a[i1]), bl[j1], pp[(q + 1) & 1], 0, 0, 0);
+                for (int i = 0; i < kMI; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(sacc[i][j][r], d, acc[i][j][r]);
+                    sacc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
                 }
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[q / kWT][q % kWT][r] = fmaf(pp[q & 1][r], d[q % kWT], acc[q / kWT][q % kWT][r]);
             }
         }
     };
@@ -354,7 +366,10 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     };
     // Split x, the step's one block: per subtile the hi and the lo fragments times the
     // same fp16 codes, chained into one fp32 sum (exact products), then the rescale.
-    // Q6_K: q * scale as fp16 hi + lo codes, four chained MFMAs per subtile.
+    // Q6_K: q * scale as fp16 hi + lo codes, four chained MFMAs per subtile.  (Chaining
+    // a super-block's blocks as on bf16 x was slower here: 194 -> 225 us at M = 512;
+    // these four MFMAs per block outweigh the rescale, and the chained sums' registers
+    // rule out the 128 x 96 tiles.)
     auto compute_x2 = [&](const BRegs<kFmt, kWB, kWT>& B, const AFrags& ah, const AFrags& al) {
         if constexpr (kX2) {
             constexpr int kCodes = F::kQ6K ? 2 : 1;
@@ -412,6 +427,9 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
     constexpr int kBLoads = kWT * (kWB * F::kLoadsPerBlock + F::kLoadsPerTile);
     static_assert(kBLoads <= 63, "vmcnt counts up to 63");
     const int u_last = max(u1 - 1, 0);
+    // Q6_K: unit u holds blocks u kWB .. u kWB + kWB - 1 of the row; a super-block is 8
+    // blocks, and a K part may start or end inside one
+    auto q6_ends = [&](int u) { return kChain && (((u + 1) * kWB) % 8 == 0 || u == u1 - 1); };
     auto step = [&](int it, const BRegs<kFmt, kWB, kWT>& cur, BRegs<kFmt, kWB, kWT>& far) {
         const int u = u0 + it;
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kBLoads));
@@ -435,6 +453,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
             asm volatile("" ::: "memory");
             load_b(far, min(u + 2, u_last));
             asm volatile("" ::: "memory");
+            if (live && q6_ends(u)) flush_q6(cur);
             return;
         }
         AFrags a;
@@ -459,6 +478,7 @@ __global__ __launch_bounds__(64 * kNW * kKS, 512 / (64 * kNW * kKS)) void gemm_k
                 compute(cur, a, tt);
                 __builtin_amdgcn_s_setprio(0);
             }
+        if (live && q6_ends(u)) flush_q6(cur);
     };
 
     BRegs<kFmt, kWB, kWT> b0, b1, b2;
@@ -570,21 +590,24 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, fl
 // The relative costs are fitted to shape-by-shape timings on MI355X (Q4_0 / Q8_0,
 // M = 128..2048, 4096..28672 rows): the model picks the fastest shape in 11 of 12
 // cases and is within 10% in the twelfth.  Fixed per shape, so a row's bits depend
-// only on m and the weight.
+// only on m and the weight.  A shape with per_cu < 0 is not built for the format
+// (Q6_K on bf16 x has no 128 x 96 tiles: its super-block sums take 96 more registers
+// and would spill).
 int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4]) {
     static const int bm[4] = {128, 128, 64, 64}, wt[4] = {3, 2, 3, 2};
     static const double cost_per_flop[4] = {1.00, 1.10, 1.25, 1.35};
     const int64_t cus = 256;
-    int best = 0;
+    int best = -1;
     double best_cost = 0.0;
     for (int i = 0; i < 4; ++i) {
+        if (per_cu[i] < 0) continue;
         const int spc = per_cu[i] > 0 ? per_cu[i] : 1;
         const int64_t wgs = (w.n_tiles + 2 * wt[i] - 1) / (2 * wt[i]) * ((m + bm[i] - 1) / bm[i]);
         const int64_t slots = cus * spc;
         const double round = (double)spc * bm[i] * wt[i] * cost_per_flop[i] * (spc == 1 ? 1.2 : 1.0);
         double cost = (double)(wgs / slots) * round;
         if (wgs % slots) cost += round * (wgs % slots <= cus ? 0.67 : 1.0);
-        if (i == 0 || cost < best_cost) best = i, best_cost = cost;
+        if (best < 0 || cost < best_cost) best = i, best_cost = cost;
     }
     return best;
 }
@@ -596,11 +619,23 @@ int blocks_per_cu(const void* kernel, int threads) {
     return n;
 }
 
+// Shape 0 is built for every instance but Q6_K on bf16 x.
+template <int kFmt, bool kX2>
+constexpr bool kWideTiles = kFmt != OPENMINI_QMM_Q6_K || kX2;
+
+template <int kFmt, bool kGate, bool kX2>
+int shape0_per_cu() {
+    if constexpr (kWideTiles<kFmt, kX2>)
+        return blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 3, kGate, kX2>, 256);
+    else
+        return -1;
+}
+
 // Workgroups per CU of the four shapes' kernels (queried once per instantiation).
 template <int kFmt, bool kGate, bool kX2>
 const int (&shape_occupancy())[4] {
     static const int per_cu[4] = {
-        blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 3, kGate, kX2>, 256),
+        shape0_per_cu<kFmt, kGate, kX2>(),
         blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 2, kGate, kX2>, 256),
         blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 3, kGate, kX2>, 512),
         blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 2, kGate, kX2>, 512)};
@@ -611,7 +646,9 @@ template <int kFmt, bool kGate, bool kX2>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
                        hipStream_t s) {
     switch (choose_shape(w, m, shape_occupancy<kFmt, kGate, kX2>())) {
-    case 0: return launch_shape<kFmt, 128, 2, 2, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case 0:
+        if constexpr (kWideTiles<kFmt, kX2>) return launch_shape<kFmt, 128, 2, 2, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+        return hipErrorInvalidValue;
     case 1: return launch_shape<kFmt, 128, 2, 2, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
     case 2: return launch_shape<kFmt, 64, 2, 4, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
     default: return launch_shape<kFmt, 64, 2, 4, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);

@@ -231,7 +231,9 @@ def test_gemm_every_launch_shape(qmm, orc, qtype, split_x):
     """The prefill GEMM picks one of four launch shapes (128 or 64 rows x 3 or 2 weight
     tiles per wave) from the problem size.  Over these sizes every shape must be picked
     at least once, for every weight type, with bf16 and with split fp32 activations,
-    and every call meets the oracle (sampled rows, y NaN-filled)."""
+    and every call meets the oracle (sampled rows, y NaN-filled).  Q6_K on bf16
+    activations has no 128 x 96 shape (its per-super-block sums would not fit the
+    registers)."""
     L = _native.lib()
     K = 512
     seen = {}
@@ -256,4 +258,4 @@ def test_gemm_every_launch_shape(qmm, orc, qtype, split_x):
         assert np.all(np.isfinite(y)), "unwritten (NaN) outputs"
         assert_parity(y[rows], ref, TOL, f"shape {shape} N={N} M={M}")
         seen.setdefault(shape, (N, M))
-    assert sorted(seen) == [0, 1, 2, 3], seen
+    assert sorted(seen) == ([1, 2, 3] if qtype == 14 and not split_x else [0, 1, 2, 3]), seen
