@@ -15,8 +15,9 @@
 //     12.0-12.2 -> 11.4 us, Q4_K b = 8 12.4-12.5 -> 11.7-12.1 us).
 //   * K-quant weights (the reference's reading, quant.rs:338-410 and :515-600) use
 //     their 32-element sub-blocks as the blocks, with block factor d * scale (exact).
-//     Q6_K's scale changes every 16 elements, inside one MFMA's 32: each half runs its
-//     own MFMA pair with the other half's codes zeroed, scaled by its own factor.
+//     Q6_K's scale changes every 16 elements, inside one MFMA's 32: q * scale (at most
+//     12 significant bits) goes in as fp16 hi + lo codes, four MFMAs per block, and
+//     with no per-block factor left the group's blocks chain into one D, times d.
 //     Q5_K shares Q6_K's chunk layout but has one scale per 32 elements: one MFMA
 //     pair per block, like Q4_K.
 //   * Per (batch row, 4-block group) the activations are scaled by 2^s, s chosen so
@@ -374,16 +375,42 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                 transpose4(e[0], e[1], e[2], e[3]);
                 transpose4(o[0], o[1], o[2], o[3]);
             }
+            if constexpr (F::kQ6K && !F::kQ5) {
+                // Q6_K: the scale changes every 16 elements, inside an MFMA's 32, so it
+                // goes into the codes: q * scale, an integer of at most 12 significant
+                // bits, as fp16 hi = the rounded product and lo = the exact remainder
+                // (an fp16 FMA).  With exact operands the group's 4 blocks chain into
+                // one D per tile (hi and lo activations times hi and lo codes), and d
+                // (one per row and super-block) applies once, with the range scale.
+                // lane (kq, i) takes the scale of half kq / 2 of slot (t, i)
+                float sw[4];
+                broadcast4(__uint_as_float(st.sc[i]), sw);
+                f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const f16x8 b = codes_q6(e[t], o[t], kq);
+                    const _Float16 sc = (_Float16)(float)(int8_t)((__float_as_uint(sw[t]) >> ((kq >> 1) * 8)) & 0xFFu);
+                    const f16x8 s8 = f16x8{sc, sc, sc, sc, sc, sc, sc, sc};
+                    const f16x8 bh = b * s8;
+                    const f16x8 bl = __builtin_elementwise_fma(b, s8, -bh);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bh, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bh, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bl, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bl, d, 0, 0, 0);
+                }
+                const float dd = f16_bits_to_f32((uint16_t)st.dk[i]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(d[r], rs[r] * dd, acc[i][r]);
+                continue;
+            }
             // the block factors of column i (slot (t, i) for t = 0..3), exact in fp32:
-            // the fp16 scale; Q4_K d * scale; Q6_K d * scale of each 16-element half;
-            // Q5_K d * scale (one per 32-element sub-block: its two scale bytes are equal)
-            float ds[4], ds1[4];
+            // the fp16 scale; Q4_K d * scale; Q5_K d * scale (one per 32-element
+            // sub-block: its two scale bytes are equal)
+            float ds[4];
             if constexpr (F::kQ4K) {
                 broadcast4(f16_bits_to_f32((uint16_t)st.dk[i]) * (float)(st.sc[i] & 0xFFu), ds);
             } else if constexpr (F::kQ6K) {
-                const float dd = f16_bits_to_f32((uint16_t)st.dk[i]);
-                broadcast4(dd * (float)(int8_t)(st.sc[i] & 0xFFu), ds);
-                if constexpr (!F::kQ5) broadcast4(dd * (float)(int8_t)((st.sc[i] >> 8) & 0xFFu), ds1);
+                broadcast4(f16_bits_to_f32((uint16_t)st.dk[i]) * (float)(int8_t)(st.sc[i] & 0xFFu), ds);
             } else {
                 broadcast4(f16_bits_to_f32((uint16_t)st.sc[i]), ds);
             }
@@ -403,24 +430,10 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                     b = codes_q6(e[t], o[t], kq);
                 else
                     b = codes_q8(e[t], o[t]);
-                if constexpr (F::kQ6K && !F::kQ5) {
-                    // the halves carry their own factors: lanes kq = 0, 1 hold the
-                    // block's elements 0..15, lanes 2, 3 elements 16..31; one MFMA pair
-                    // per half with the other half's codes zeroed
-                    const f16x8 z = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                    const f16x8 b0 = kq < 2 ? b : z, b1 = kq < 2 ? z : b;
-                    f32x4 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b0, d0, 0, 0, 0);
-                    f32x4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b1, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b1, d1, 0, 0, 0);
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) gs[r] = fmaf(d1[r], ds1[t], fmaf(d0[r], ds[t], gs[r]));
-                } else {
-                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], b, d, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds[t], gs[r]);
-                }
+                for (int r = 0; r < 4; ++r) gs[r] = fmaf(d[r], ds[t], gs[r]);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(gs[r], rs[r], acc[i][r]);
