@@ -235,8 +235,14 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
     const int tile0 = tgroup * T;
     const int gs0 = (int)((int64_t)groups * split / splits);
     const int gsn = (int)((int64_t)groups * (split + 1) / splits) - gs0;
-    const int g0 = gs0 + (int)((int64_t)gsn * wave / W);
-    const int g1 = gs0 + (int)((int64_t)gsn * (wave + 1) / W);
+    // Eight waves walk the split's K range as two halves of four waves, each half cut
+    // as a two-way split cuts K for four waves: an eight-wave workgroup then computes
+    // bitwise what two four-wave splits compute (choose_batch_shape relies on it).
+    constexpr int kWH = W == 8 ? 4 : W;  // waves per half
+    const int hs0 = gs0 + (int)((int64_t)gsn * (wave / kWH) / (W / kWH));
+    const int hsn = gs0 + (int)((int64_t)gsn * (wave / kWH + 1) / (W / kWH)) - hs0;
+    const int g0 = hs0 + (int)((int64_t)hsn * (wave % kWH) / kWH);
+    const int g1 = hs0 + (int)((int64_t)hsn * (wave % kWH + 1) / kWH);
 
     const __amdgpu_buffer_rsrc_t w_rs0 = make_rsrc(w0, (uint32_t)n_tiles * groups * kChunk);
     const __amdgpu_buffer_rsrc_t w_rs1 = make_rsrc(kNW == 2 ? w1 : w0, (uint32_t)n_tiles * groups * kChunk);
@@ -464,7 +470,8 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the unconsumed prefetch has landed
     }
 
-    // The W K slices meet in LDS and are added in wave order.
+    // The W K slices meet in LDS and are added in wave order (eight waves: each half
+    // in wave order, then the two halves, as the K split adds its splits).
     __syncthreads();  // every wave is done with its scale slots
 #pragma unroll
     for (int i = 0; i < kNT; ++i)
@@ -482,7 +489,13 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
         for (int nw = 0; nw < kNW; ++nw) {
             v[nw] = lds[(nw * T + i) * 256 + src];
 #pragma unroll
-            for (int w = 1; w < W; ++w) v[nw] += lds[((w * kNT) + nw * T + i) * 256 + src];
+            for (int w = 1; w < kWH; ++w) v[nw] += lds[((w * kNT) + nw * T + i) * 256 + src];
+            if constexpr (W == 8) {
+                float h = lds[((4 * kNT) + nw * T + i) * 256 + src];
+#pragma unroll
+                for (int w = 5; w < 8; ++w) h += lds[((w * kNT) + nw * T + i) * 256 + src];
+                v[nw] += h;
+            }
         }
         if constexpr (kNW == 2)
             y[(size_t)b * n_rows + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
@@ -611,7 +624,8 @@ static int64_t tiles_per_cu(int type, int64_t n_tiles, bool pair) {
 // tile per workgroup; there the K split alone fills them: 1024 x 8192 (64 tiles, 4
 // splits) Q4_0 B = 16 17.1 -> 10.0 us, B = 4 10.0 -> 7.8 us, Q8_0 B = 8 11.6 -> 8.4 us
 // (2 splits of 2 tiles: 12.9 us, 4 splits of 2 tiles 10.4 us at B = 16).  The choice
-// depends on the shape only, so results stay bitwise independent of the batch size.
+// depends on the shape only, so results stay bitwise independent of the batch size
+// (choose_batch_shape's eight-wave form of a split at 4 rows computes the same bits).
 void batch_split(int type, int64_t n_tiles, int64_t groups, int* t, int* s) {
     const int64_t t0 = tiles_per_cu(type, n_tiles, false);
     const bool nib = type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q4_K || type == OPENMINI_QMM_Q4_1;
@@ -644,6 +658,18 @@ BatchShape choose_batch_shape(const Weight& w, int batch, bool pair) {
     } else {
         sh.t = w.split_t;
         sh.split = w.split_s;
+    }
+    // At most 4 rows, a two-way split of 64-127 K groups over tile groups of 2+ tiles
+    // runs as one workgroup of eight waves on half the tiles instead: the same K cut
+    // and addition order (gemv_batch_kernel), so the bits equal the split's, and no
+    // hand-off.  Interleaved A/B passes on two boxes (us, split -> eight waves):
+    // Q4_0 8192 x 8192 b = 4 16.0-17.1 -> 13.7-14.5, Q4_K 16.2-16.8 -> 14.3-14.7,
+    // 4096 x 8192 10.3-10.6 -> 9.3-9.5, 4096 x 11008 Q8_0 15.0-15.5 -> 14.0-14.5, Q6_K
+    // 18.1-20.2 -> 16.8-17.8, Q4_0 even; at 8 rows 4096 x 11008 lost 10-20% and 8192 x
+    // 8192 was even, at 16 rows both lost.
+    if (!pair && batch <= 4 && sh.split == 2 && sh.t >= 2 && w.groups >= 64 && w.groups < 128) {
+        sh.split = 1;
+        sh.t /= 2;
     }
     sh.w = w.groups >= 8 ? 4 : 1;
     // at least 64 K groups per workgroup: eight waves of 8+ groups each (two per SIMD)

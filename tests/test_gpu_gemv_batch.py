@@ -82,6 +82,9 @@ def test_batch_tiles_per_workgroup(qmm, orc, qtype, N, K, B):
     (Q8_0, 2000, 16384),       # 2 splits of 1 tile, 64 groups each: eight waves
     (14, 4096, 16384),         # Q6_K, 2 splits of 2 tiles, eight waves
     (12, 9600, 8192),          # Q4_K, 600 tiles (3 per workgroup), no split, eight waves
+    (Q4_0, 8192, 8192),        # 2 splits of 4 tiles, 64 groups; at 4 rows one workgroup of 8 waves
+    (Q8_0, 4096, 11008),       # 2 splits of 2 tiles, 86 groups (43 per split); the same at 4 rows
+    (Q4_0, 4112, 8192),        # 257 tiles (ragged): 2 splits of 4 tiles; the same at 4 rows
 ])
 def test_batch_k_split(qmm, orc, qtype, N, K):
     """The K-split launches (two or four workgroups per tile group, each over a part
@@ -90,7 +93,8 @@ def test_batch_k_split(qmm, orc, qtype, N, K):
     of 64+ K groups.  Every call is checked on all outputs, y NaN-filled first:
     against the oracle at 4, 7 and 16 rows, and bit for bit against a repeat of the
     same call and against the 16-row call's rows (the split depends on the shape
-    only).  The calls run back to back on one weight, so each starts from the count
+    only; at 4 rows a two-way split of 64-127 groups runs as one eight-wave workgroup
+    per tile group, which must give the split's bits).  The calls run back to back on one weight, so each starts from the count
     its predecessors left (0, splits, 2 splits, ...): a wrong choice of last
     workgroup would leave outputs unwritten (NaN) or half-summed."""
     blocks = (synth.kquant_blocks(qtype, N, K, seed=0xB700 + N) if qtype in (12, 14)
