@@ -59,6 +59,9 @@ __device__ __forceinline__ f16x8 codes_q4_perm(uint32_t w) {
     return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
 }
 
+// Bits 0..3 of v (v < 16) to bit 0 of bytes 0..3.
+__device__ __forceinline__ uint32_t spread4(uint32_t v) { return (v * 0x00204081u) & 0x01010101u; }
+
 // 8 Q8_0 codes (two words, int8) -> 8 fp16 q.
 __device__ __forceinline__ f16x8 codes_q8(uint32_t w0, uint32_t w1) {
     const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;  // q + 128

@@ -159,7 +159,7 @@ struct Fmt {
                                   : kQ6                     ? kQ6KChunk
                                   : kQ41                    ? kQ41Chunk
                                                             : chunk_bytes_for(kFmt == OPENMINI_QMM_Q4_0);
-    static constexpr int kDOff = kCodeBytes + (kQ6 ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
+    static constexpr int kDOff = kQ5 ? kQ5KDOff : kCodeBytes + (kQ6 ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
     static constexpr int kCodeShift = kNib ? 4 : kQ6 ? 2 : 0;
 };
 
@@ -175,7 +175,12 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
     constexpr int kChunk = F::kChunk;
     constexpr int kS = kSlots<B, P>;
     constexpr int kZero = kS - 1;
-    __shared__ uint4 a_lds[W][kS];
+    // Q5_K with eight waves holds 56 KB of LDS so that at most two workgroups share a
+    // CU.  Its 72 registers would let three in, and on 256-workgroup grids (4096-row
+    // weights) the room was filled unevenly: interleaved A/B on one box, 4096 x 11008
+    // b = 1 11.4 -> 9.4 us, b = 2 14.2 -> 11.7 us; 11008 x 4096 b = 1 8.3 -> 8.5-8.8 us.
+    constexpr int kSAlloc = F::kQ5 && W == 8 && kS < 56 * 1024 / 16 / W ? 56 * 1024 / 16 / W : kS;
+    __shared__ uint4 a_lds[W][kSAlloc];
     __shared__ float red[W][kNW][B][16];
 
     const int lane = threadIdx.x & 63;
@@ -279,11 +284,15 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                 if constexpr (kFmt == OPENMINI_QMM_Q8_0)
                     c[nw][p][1] = __builtin_bit_cast(
                         uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rs[nw], lane * 32 + 16, soff, 0));
-                if constexpr (F::kQ6)
+                if constexpr (F::kQ5)  // the slot's high-bit byte
+                    hb[nw][p].x = __builtin_amdgcn_raw_buffer_load_b8(w_rs[nw], kQ5KQhOff + lane, soff, 0);
+                else if constexpr (F::kQ6)
                     hb[nw][p] = __builtin_bit_cast(
                         uint2, __builtin_amdgcn_raw_buffer_load_b64(w_rs[nw], kTileEntries * 16 + lane * 8, soff, 0));
                 if constexpr (kFmt == OPENMINI_QMM_Q4_K)
                     sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b8(w_rs[nw], kCodeBytes + lane, soff, 0);
+                else if constexpr (F::kQ5)
+                    sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b8(w_rs[nw], kQ5KScaleOff + lane, soff, 0);
                 else
                     sc[nw][p] = __builtin_amdgcn_raw_buffer_load_b16(w_rs[nw], kCodeBytes + lane * 2, soff, 0);
                 if constexpr (F::kKQ)
@@ -344,7 +353,17 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* __restrict_
                     // 4 q as int8 bytes: low 4 bits of the 6-bit code at bits 2..5, its top
                     // 2 bits at 6..7 (field f of top-bit word m: element 16 m + 4 f + i)
                     const uint4 w = c[nw][p][0];
-                    const uint2 h = hb[nw][p];
+                    uint2 h = hb[nw][p];
+                    if constexpr (F::kQ5) {
+                        // Q5_K: the top 2 bits of the code q - 16 are 3 where the element's
+                        // high bit is 0, else 0; element e's high bit is bit e % 8 of the
+                        // slot's byte, so both top-bit words are one word: byte i =
+                        // 0x33 (1 - bit i) + 0xCC (1 - bit 4 + i)
+                        const uint32_t nb = ~h.x & 0xFFu;
+                        const uint32_t x2 = spread4(nb & 0xFu) | (spread4(nb >> 4) << 2);
+                        const uint32_t y2 = x2 | (x2 << 1);
+                        h.x = h.y = y2 | (y2 << 4);
+                    }
                     auto lo = [](uint32_t wj, uint32_t hm, int sh) {
                         return (int)(((wj << 2) & 0x3C3C3C3Cu) | ((hm << sh) & 0xC0C0C0C0u));
                     };

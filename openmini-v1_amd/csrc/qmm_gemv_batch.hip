@@ -165,8 +165,8 @@ struct BFmt {
     static constexpr bool kMin = kQ41 || kQ5;    // block minimum
     static constexpr bool kNib = !kQ8 && !kQ6K;  // Q4_0 / Q4_1 / Q4_K: the codes are nibbles q ^ 8
     static constexpr int kCB = kQ8 ? 32 : 16;      // bytes of a slot's (low) codes
-    static constexpr int kScaleOff = kTileEntries * (kQ6K ? 24 : kCB);
-    static constexpr int kDOff = kScaleOff + (kQ6K ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
+    static constexpr int kScaleOff = kQ5 ? kQ5KScaleOff : kTileEntries * (kQ6K ? 24 : kCB);
+    static constexpr int kDOff = kQ5 ? kQ5KDOff : kScaleOff + (kQ6K ? 2 : 1) * kTileEntries;  // K-quant: fp16 d per row
     static constexpr int kChunk = kQ4K ? kQ4KChunk : kQ5 ? kQ5KChunk : kQ6K ? kQ6KChunk : kQ41 ? kQ41Chunk
                                                                                           : chunk_bytes_for(!kQ8);
 };
@@ -175,7 +175,7 @@ template <int kFmt, int kNT, int kXB>
 struct Stage {
     float x[kXB][8];
     uint4 c[kNT][BFmt<kFmt>::kQ8 ? 2 : 1];
-    uint2 hb[BFmt<kFmt>::kQ6K ? kNT : 1];  // Q6_K: the slot's top code bits
+    uint2 hb[BFmt<kFmt>::kQ6K ? kNT : 1];  // Q6_K: the slot's top code bits; Q5_K: its high-bit byte
     uint32_t sc[kNT];
     uint32_t dk[BFmt<kFmt>::kKQ ? kNT : 1];  // K-quant: the fp16 d of the slot's row
     uint32_t mn[BFmt<kFmt>::kMin ? kNT : 1];  // Q4_1: the slot's fp16 m; Q5_K: its minimum nibble
@@ -189,6 +189,18 @@ __device__ __forceinline__ f16x8 codes_q6(uint32_t w, uint32_t hm, int kq) {
     const int f = (kq & 1) * 4;  // bit of field 2 (kq & 1); field + 1 for elements + 4..7
     const uint32_t lo = ((w & 0x0F0F0F0Fu) | (((hm >> f) & 0x03030303u) << 4)) ^ 0x20202020u;
     const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) | (((hm >> (f + 2)) & 0x03030303u) << 4)) ^ 0x20202020u;
+    uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1056.0f),
+                     pk_sub(magic_pair(hi, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1056.0f)};
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
+}
+
+// Q5_K low-nibble word kq of a slot and its high-bit byte -> 8 fp16 q - 16, elements
+// 8 kq .. 8 kq + 7 (element e's high bit is bit e % 8: bits 0..3 for the low nibbles,
+// 4..7 for the high ones): bytes u = q4 + 16 + 16 bit through the 1024 + u pattern,
+// minus 1056.
+__device__ __forceinline__ f16x8 codes_q5(uint32_t w, uint32_t qh) {
+    const uint32_t lo = (w & 0x0F0F0F0Fu) | ((spread4(qh & 0xFu) << 4) + 0x10101010u);
+    const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | ((spread4((qh >> 4) & 0xFu) << 4) + 0x10101010u);
     uint32_t p[4] = {pk_sub(magic_pair(lo, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(lo, kSel23), (_Float16)1056.0f),
                      pk_sub(magic_pair(hi, kSel01), (_Float16)1056.0f), pk_sub(magic_pair(hi, kSel23), (_Float16)1056.0f)};
     return __builtin_bit_cast(f16x8, *reinterpret_cast<uint4*>(p));
@@ -290,10 +302,12 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             if constexpr (F::kQ8)
                 st.c[i][1] =
                     __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane * kCB + 16, soff, 0));
-            if constexpr (F::kQ6K)
+            if constexpr (F::kQ5)
+                st.hb[i].x = __builtin_amdgcn_raw_buffer_load_b8(rs, kQ5KQhOff + lane, soff, 0);
+            else if constexpr (F::kQ6K)
                 st.hb[i] = __builtin_bit_cast(
                     uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, kCodeBytes + lane * 8, soff, 0));
-            if constexpr (F::kQ4K)
+            if constexpr (F::kQ4K || F::kQ5)
                 st.sc[i] = __builtin_amdgcn_raw_buffer_load_b8(rs, F::kScaleOff + lane, soff, 0);
             else
                 st.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, F::kScaleOff + lane * 2, soff, 0);
@@ -369,7 +383,13 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
             if constexpr (!F::kQ8) {
                 e[0] = st.c[i][0].x; e[1] = st.c[i][0].y; e[2] = st.c[i][0].z; e[3] = st.c[i][0].w;
                 transpose4(e[0], e[1], e[2], e[3]);
-                if constexpr (F::kQ6K) {
+                if constexpr (F::kQ5) {
+                    // lane (kq, i) takes the high-bit byte of slot (t, i)
+                    float hb4[4];
+                    broadcast4(__uint_as_float(st.hb[i].x), hb4);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) o[t] = __float_as_uint(hb4[t]);
+                } else if constexpr (F::kQ6K) {
                     // lane (kq, i) takes top-bit word kq / 2 of slot (t, i): the loader
                     // lane's registers are words 0, 0, 1, 1 before the transpose
                     o[0] = st.hb[i].x; o[1] = st.hb[i].x; o[2] = st.hb[i].y; o[3] = st.hb[i].y;
@@ -433,7 +453,7 @@ __global__ __launch_bounds__(64 * W) void gemv_batch_kernel(const uint8_t* __res
                 if constexpr (F::kNib)
                     b = codes_q4_perm(e[t]);  // the activations were loaded in its order
                 else if constexpr (F::kQ6K)
-                    b = codes_q6(e[t], o[t], kq);
+                    b = F::kQ5 ? codes_q5(e[t], o[t]) : codes_q6(e[t], o[t], kq);
                 else
                     b = codes_q8(e[t], o[t]);
                 f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);

@@ -53,10 +53,12 @@
 //   Q5_K (176-byte super-blocks, the reference's reading quant.rs:433-505): element i
 //     of sub-block sb has q = (nibble of byte 36 + 16 sb + i / 2, even i high) + 16 *
 //     (bit i % 8 of byte 20 + sb) and value (q - 16) * d * (byte 4 + sb & 0x3F) +
-//     dmin * (nibble sb % 2 of byte 12 + sb / 2).  Stored as a Q6_K chunk whose 6-bit
-//     code is q - 16 (low nibble q & 15, top bits 0 or 3) with the sub-block scale in
-//     both halves, then 16 x fp16 dmin (per row) and 64 x u8 minimum nibbles.  The
-//     code term is exact as (q - 16) * (d * scale).  1792 B per chunk.
+//     dmin * (nibble sb % 2 of byte 12 + sb / 2).  In that reading a sub-block's 32
+//     high bits are the 8 bits of one byte, each used by 4 elements.  Slot codes: Q6_K's
+//     16 B of low nibbles (the nibble of q), then 64 x u8 high-bit bytes (the
+//     sub-block's byte 20 + sb as it stands), 64 x u8 scales, 64 x u8 minimum nibbles,
+//     16 x fp16 d, 16 x fp16 dmin (per row).  The code term is exact as
+//     (q - 16) * (d * scale).  1280 B per chunk (the GGUF bytes: 1408).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -154,13 +156,16 @@ __host__ __device__ constexpr int chunk_bytes_for(bool q4) { return kTileEntries
 // K-quant chunks: codes, per-slot scale bytes, then one fp16 d per tile row.
 constexpr int kQ4KChunk = kTileEntries * 16 + kTileEntries + 2 * kTileRows;       // 1120
 constexpr int kQ6KChunk = kTileEntries * 24 + 2 * kTileEntries + 2 * kTileRows;   // 1696
-// Block-minimum chunks: Q4_1 = a Q4_0 chunk + 64 fp16 m; Q5_K = a Q6_K chunk + 16 fp16
-// dmin (per row) + 64 u8 minimum nibbles.
+// Block-minimum chunks: Q4_1 = a Q4_0 chunk + 64 fp16 m; Q5_K: low nibbles, then
+// per-slot high-bit byte, scale and minimum, then per-row d and dmin.
 constexpr int kQ41MinOff = kTileEntries * 16 + 2 * kTileEntries;                    // 1152
 constexpr int kQ41Chunk = kQ41MinOff + 2 * kTileEntries;                            // 1280
-constexpr int kQ5KDminOff = kQ6KChunk;                                              // 1696
-constexpr int kQ5KMinOff = kQ5KDminOff + 2 * kTileRows;                             // 1728
-constexpr int kQ5KChunk = kQ5KMinOff + kTileEntries;                                // 1792
+constexpr int kQ5KQhOff = kTileEntries * 16;                                        // 1024
+constexpr int kQ5KScaleOff = kQ5KQhOff + kTileEntries;                              // 1088
+constexpr int kQ5KMinOff = kQ5KScaleOff + kTileEntries;                             // 1152
+constexpr int kQ5KDOff = kQ5KMinOff + kTileEntries;                                 // 1216
+constexpr int kQ5KDminOff = kQ5KDOff + 2 * kTileRows;                               // 1248
+constexpr int kQ5KChunk = kQ5KDminOff + 2 * kTileRows;                              // 1280
 inline int chunk_bytes(int type) {
     switch (type) {
     case OPENMINI_QMM_Q4_K: return kQ4KChunk;

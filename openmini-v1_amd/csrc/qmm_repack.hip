@@ -201,9 +201,8 @@ __device__ __forceinline__ void lds_words(const uint8_t* base, int a, uint32_t* 
 //        byte 4 + sb & 0x3F, minimum = nibble sb % 2 of byte 12 + sb / 2 (even sb: low),
 //        element i: q4 = nibble of byte 36 + 16 sb + i / 2 (even i: high), high bit =
 //        bit i % 8 of byte 20 + sb; value (q4 + 16 bit - 16) d scale + dmin minimum.
-//        Written as a Q6_K chunk with 6-bit code q4 + 16 bit - 16 (low nibble q4, top
-//        bits 0 for bit 1, 3 for bit 0), the scale in both halves, then dmin per row
-//        and the minimum per slot.
+//        Written as Q6_K's low nibbles (q4), the high-bit byte, scale and minimum per
+//        slot, then d and dmin per row.
 //   Q8_K quant.rs:768-800: d = fp16 at 0, element i = int8 byte 2 + i, value q d.
 //        Written as a Q8_0 chunk: the codes of 32-element sub-block sb as they stand,
 //        d as every slot's scale.
@@ -311,16 +310,8 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
                 const uint32_t hi = (rr & 0x00F000F0u) | ((rr << 4) & 0xF000F000u);
                 w[j] = lo | hi;
             }
-            // top bits of element 16 m + 4 f + i: 3 * (1 - bit (4 f + i) % 8 of the qh
-            // byte), the same for both words: byte i = 51 nb_i + 204 nb_(4 + i) with
-            // nb = the inverted qh bits
-            const uint32_t nb = ~(uint32_t)st8[blk + 20 + sub] & 0xFFu;
-            uint32_t top = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) top |= (51u * ((nb >> i) & 1u) + 204u * ((nb >> (4 + i)) & 1u)) << (8 * i);
-            w[4] = w[5] = top;
-            const uint32_t s6 = st8[blk + 4 + sub] & 0x3Fu;
-            sc = s6 | (s6 << 8);
+            w[4] = st8[blk + 20 + sub];  // the high-bit byte, as it stands
+            sc = st8[blk + 4 + sub] & 0x3Fu;
             const uint32_t mb = st8[blk + 12 + (sub >> 1)];
             mn = (sub & 1) ? (mb >> 4) : (mb & 0x0Fu);
             dbits = d;
@@ -355,7 +346,17 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
             dbits = d;
         }
     }
-    if constexpr (kQ8K) {
+    if constexpr (kQ5) {
+        reinterpret_cast<uint4*>(ch)[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        ch[kQ5KQhOff + e] = (uint8_t)w[4];
+        ch[kQ5KScaleOff + e] = (uint8_t)sc;
+        ch[kQ5KMinOff + e] = (uint8_t)mn;
+        if ((e >> 4) == 0) {
+            reinterpret_cast<uint16_t*>(ch + kQ5KDOff)[r] = dbits;
+            reinterpret_cast<uint16_t*>(ch + kQ5KDminOff)[r] = dmbits;
+        }
+        return;
+    } else if constexpr (kQ8K) {
         uint4* c4 = reinterpret_cast<uint4*>(ch + e * 32);
         c4[0] = make_uint4(w[0], w[1], w[2], w[3]);
         c4[1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -370,10 +371,6 @@ __global__ __launch_bounds__(kRepackThreads) void repack_kquant_kernel(const uin
         reinterpret_cast<uint16_t*>(ch + kScaleOff)[e] = (uint16_t)sc;
     }
     if ((e >> 4) == 0) reinterpret_cast<uint16_t*>(ch + kDOff)[r] = dbits;
-    if constexpr (kQ5) {
-        ch[kQ5KMinOff + e] = (uint8_t)mn;
-        if ((e >> 4) == 0) reinterpret_cast<uint16_t*>(ch + kQ5KDminOff)[r] = dmbits;
-    }
 }
 
 // Chunked weight -> f32 [n][k] (8 * nwords outputs, row-major; one code word = 8
