@@ -586,14 +586,19 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, fl
 // cost more per flop (each B fragment serves fewer MFMAs, each A fragment fewer
 // tiles).  The model: workgroups run in rounds of (CUs x workgroups per CU, from the
 // kernel's occupancy); a round costs (workgroups per CU) x (tile work) x (the shape's
-// relative cost per flop), a last round of at most one workgroup per CU 0.67 of that.
+// relative cost per flop), a last round of at most one workgroup per CU 0.67 of that
+// where a CU holds two (a workgroup alone on its CU runs faster than two sharing it).
+// On bf16 x, a last round of a shape that runs one workgroup per CU costs a full one
+// (Q8_0 / Q4_K / Q6_K 64 x 96 tiles: 2 rounds took twice 1 round, so the discount had
+// it picked over faster shapes at M = 160..640).  Split x keeps the discount there:
+// with it the shapes it picks measured faster at 11008 rows, M = 256.
 // The relative costs are fitted to shape-by-shape timings on MI355X (Q4_0 / Q8_0,
 // M = 128..2048, 4096..28672 rows): the model picks the fastest shape in 11 of 12
 // cases and is within 10% in the twelfth.  Fixed per shape, so a row's bits depend
 // only on m and the weight.  A shape with per_cu < 0 is not built for the format
 // (Q6_K on bf16 x has no 128 x 96 tiles: its super-block sums take 96 more registers
 // and would spill).
-int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4]) {
+int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4], bool split_x) {
     static const int bm[4] = {128, 128, 64, 64}, wt[4] = {3, 2, 3, 2};
     static const double cost_per_flop[4] = {1.00, 1.10, 1.25, 1.35};
     const int64_t cus = 256;
@@ -606,7 +611,7 @@ int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4]) {
         const int64_t slots = cus * spc;
         const double round = (double)spc * bm[i] * wt[i] * cost_per_flop[i] * (spc == 1 ? 1.2 : 1.0);
         double cost = (double)(wgs / slots) * round;
-        if (wgs % slots) cost += round * (wgs % slots <= cus ? 0.67 : 1.0);
+        if (wgs % slots) cost += round * ((spc > 1 || split_x) && wgs % slots <= cus ? 0.67 : 1.0);
         if (best < 0 || cost < best_cost) best = i, best_cost = cost;
     }
     return best;
@@ -645,7 +650,7 @@ const int (&shape_occupancy())[4] {
 template <int kFmt, bool kGate, bool kX2>
 hipError_t launch_kind(const Weight& w, const uint16_t* x, const int* x_exp, float* y, int64_t m, int64_t kx,
                        hipStream_t s) {
-    switch (choose_shape(w, m, shape_occupancy<kFmt, kGate, kX2>())) {
+    switch (choose_shape(w, m, shape_occupancy<kFmt, kGate, kX2>(), kX2)) {
     case 0:
         if constexpr (kWideTiles<kFmt, kX2>) return launch_shape<kFmt, 128, 2, 2, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
         return hipErrorInvalidValue;
@@ -829,17 +834,17 @@ hipError_t launch_gemm_bf16(const Weight& w, const uint16_t* x, float* y, int64_
 int gemm_shape(const Weight& w, int64_t m, bool split_x) {
     switch (w.type) {
     case OPENMINI_QMM_Q4_0:
-        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, true>())
-                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, false>());
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, true>(), split_x)
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_0, false, false>(), split_x);
     case OPENMINI_QMM_Q8_0:
-        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, true>())
-                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, false>());
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, true>(), split_x)
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q8_0, false, false>(), split_x);
     case OPENMINI_QMM_Q4_K:
-        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, true>())
-                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, false>());
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, true>(), split_x)
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q4_K, false, false>(), split_x);
     case OPENMINI_QMM_Q6_K:
-        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, true>())
-                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, false>());
+        return split_x ? choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, true>(), split_x)
+                       : choose_shape(w, m, shape_occupancy<OPENMINI_QMM_Q6_K, false, false>(), split_x);
     default: return -1;
     }
 }
