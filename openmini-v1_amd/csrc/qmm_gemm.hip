@@ -594,7 +594,7 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, fl
 // with it the shapes it picks measured faster at 11008 rows, M = 256.
 // The relative costs are fitted to shape-by-shape timings on MI355X (Q4_0 / Q8_0,
 // M = 128..2048, 4096..28672 rows): the model picks the fastest shape in 11 of 12
-// cases and is within 10% in the twelfth.  Fixed per shape, so a row's bits depend
+// cases and is within 2% in the twelfth.  Fixed per shape, so a row's bits depend
 // only on m and the weight.  A shape with per_cu < 0 is not built for the format
 // (Q6_K on bf16 x has no 128 x 96 tiles: its super-block sums take 96 more registers
 // and would spill).
