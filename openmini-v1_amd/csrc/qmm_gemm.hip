@@ -587,20 +587,21 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, fl
 // tiles).  The model: workgroups run in rounds of (CUs x workgroups per CU, from the
 // kernel's occupancy); a round costs (workgroups per CU) x (tile work) x (the shape's
 // relative cost per flop), a last round of at most one workgroup per CU 0.67 of that
-// where a CU holds two (a workgroup alone on its CU runs faster than two sharing it).
-// On bf16 x, a last round of a shape that runs one workgroup per CU costs a full one
-// (Q8_0 / Q4_K / Q6_K 64 x 96 tiles: 2 rounds took twice 1 round, so the discount had
-// it picked over faster shapes at M = 160..640).  Split x keeps the discount there:
-// with it the shapes it picks measured faster at 11008 rows, M = 256.
+// where a CU holds two (a workgroup alone on its CU runs faster than two sharing it);
+// at one workgroup per CU a last round costs a full one (each workgroup already has
+// its CU alone).
 // The relative costs are fitted to shape-by-shape timings on MI355X (Q4_0 / Q8_0,
-// M = 128..2048, 4096..28672 rows): the model picks the fastest shape in 11 of 12
-// cases and is within 2% in the twelfth.  Fixed per shape, so a row's bits depend
-// only on m and the weight.  A shape with per_cu < 0 is not built for the format
-// (Q6_K on bf16 x has no 128 x 96 tiles: its super-block sums take 96 more registers
-// and would spill).
+// M = 128..2048, 1024..28672 rows): on bf16 x the model picks the fastest shape in
+// 66 of 70 cases (worst +12%); split x, whose steps run twice the MFMAs, has costs of
+// its own and picks the fastest in 39 of 40 (worst +0.6%).  Fixed per shape, so a
+// row's bits depend only on m and the weight.  A shape with per_cu < 0 is not built
+// for the instance: Q6_K on bf16 x has no 128 x 96 tiles (its super-block sums take
+// 96 more registers and would spill), and split x no 64 x 96 tiles (64 x 64 ran as
+// fast or faster at every measured size).
 int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4], bool split_x) {
     static const int bm[4] = {128, 128, 64, 64}, wt[4] = {3, 2, 3, 2};
-    static const double cost_per_flop[4] = {1.00, 1.10, 1.25, 1.35};
+    static const double cost_per_flop[2][4] = {{1.00, 1.10, 1.25, 1.35},   // bf16 x
+                                               {1.00, 1.10, 1.40, 1.20}};  // split x
     const int64_t cus = 256;
     int best = -1;
     double best_cost = 0.0;
@@ -609,9 +610,9 @@ int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4], bool split_
         const int spc = per_cu[i] > 0 ? per_cu[i] : 1;
         const int64_t wgs = (w.n_tiles + 2 * wt[i] - 1) / (2 * wt[i]) * ((m + bm[i] - 1) / bm[i]);
         const int64_t slots = cus * spc;
-        const double round = (double)spc * bm[i] * wt[i] * cost_per_flop[i] * (spc == 1 ? 1.2 : 1.0);
+        const double round = (double)spc * bm[i] * wt[i] * cost_per_flop[split_x][i] * (spc == 1 ? 1.2 : 1.0);
         double cost = (double)(wgs / slots) * round;
-        if (wgs % slots) cost += round * ((spc > 1 || split_x) && wgs % slots <= cus ? 0.67 : 1.0);
+        if (wgs % slots) cost += round * (spc > 1 && wgs % slots <= cus ? 0.67 : 1.0);
         if (best < 0 || cost < best_cost) best = i, best_cost = cost;
     }
     return best;
@@ -636,13 +637,22 @@ int shape0_per_cu() {
         return -1;
 }
 
+// Shape 2 is built for bf16 x only.
+template <int kFmt, bool kGate, bool kX2>
+int shape2_per_cu() {
+    if constexpr (!kX2)
+        return blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 3, kGate, kX2>, 512);
+    else
+        return -1;
+}
+
 // Workgroups per CU of the four shapes' kernels (queried once per instantiation).
 template <int kFmt, bool kGate, bool kX2>
 const int (&shape_occupancy())[4] {
     static const int per_cu[4] = {
         shape0_per_cu<kFmt, kGate, kX2>(),
         blocks_per_cu((const void*)gemm_kernel<kFmt, 128, 2, 2, 2, 2, kGate, kX2>, 256),
-        blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 3, kGate, kX2>, 512),
+        shape2_per_cu<kFmt, kGate, kX2>(),
         blocks_per_cu((const void*)gemm_kernel<kFmt, 64, 2, 4, 2, 2, kGate, kX2>, 512)};
     return per_cu;
 }
@@ -655,7 +665,9 @@ hipError_t launch_kind(const Weight& w, const uint16_t* x, const int* x_exp, flo
         if constexpr (kWideTiles<kFmt, kX2>) return launch_shape<kFmt, 128, 2, 2, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
         return hipErrorInvalidValue;
     case 1: return launch_shape<kFmt, 128, 2, 2, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
-    case 2: return launch_shape<kFmt, 64, 2, 4, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+    case 2:
+        if constexpr (!kX2) return launch_shape<kFmt, 64, 2, 4, 2, 3, kGate, kX2>(w, x, x_exp, y, m, kx, s);
+        return hipErrorInvalidValue;
     default: return launch_shape<kFmt, 64, 2, 4, 2, 2, kGate, kX2>(w, x, x_exp, y, m, kx, s);
     }
 }
