@@ -226,6 +226,14 @@ size_t openmini_qmm_gemm_f32_workspace_bytes(int64_t m, int64_t k_cols);
  * workgroup), chosen from the problem size alone, so a row's bits depend only on m and
  * the weight.  A negative status on error. */
 int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, int split_x);
+
+/* Routing query, no counterpart in the reference: the fewest activation rows from which
+ * openmini_qmm_linear_host (and _noalloc) run the fp32 prefill GEMM on this weight
+ * rather than the decode GEMVs: 128, or 64 on weights of at least 10240 rows (N), where
+ * the GEMM's grid fills the CUs from 64 rows; 0 for Q4_1 / Q5_K, which have no prefill
+ * GEMM.  Engines that call the GEMM and GEMV entry points themselves use it to make the
+ * same choice.  A negative status on error. */
+int64_t openmini_qmm_gemm_min_rows(const openmini_qweight_t* weight);
 int openmini_qmm_gemm_f32(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t m,
                           void* d_work, size_t work_bytes, void* stream);
 
@@ -261,9 +269,10 @@ int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_
                                  void* stream);
 
 /* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
- * fp32 in/out, synchronous.  Below 128 rows the decode GEMVs, from 128 rows on the
- * fp32 prefill GEMM (openmini_qmm_gemm_f32; Q4_1 / Q5_K weights: the batched GEMV at
- * any row count); x, y and the GEMM's workspace are allocated per call. */
+ * fp32 in/out, synchronous.  Below openmini_qmm_gemm_min_rows rows (128; 64 on weights
+ * of 10240+ rows) the decode GEMVs, from there on the fp32 prefill GEMM
+ * (openmini_qmm_gemm_f32; Q4_1 / Q5_K weights: the batched GEMV at any row count); x,
+ * y and the GEMM's workspace are allocated per call. */
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,
                              int64_t m);
 
@@ -271,8 +280,8 @@ int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, f
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  x and y are staged through a
  * fixed 16 MiB device array that the library holds on every device it runs on until
- * the process ends: x, then (from 128 rows on, for the types the GEMM takes) the fp32
- * GEMM's workspace, then y, each from a 256-byte boundary.  About m * (K + N) * 4
+ * the process ends: x, then (from openmini_qmm_gemm_min_rows rows on, for the types
+ * the GEMM takes) the fp32 GEMM's workspace, then y, each from a 256-byte boundary.  About m * (K + N) * 4
  * bytes without the GEMM and m * (2 K + N + 1) * 4 with it must fit in 16 MiB, else
  * INVALID_PARAM naming the row limit.  Same kernels and results as openmini_qmm_linear_host, synchronous
  * on the null stream.

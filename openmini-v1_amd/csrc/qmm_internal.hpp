@@ -84,11 +84,19 @@ constexpr int kMaxGemvBatch = 4;  // batch rows per launch of the single-row-tun
 constexpr int kBatchRows = 16;    // batch rows per launch of the batched GEMV (its MFMA rows)
 constexpr int kMaxGroup = 4;      // weights sharing one GEMV launch
 // From this many activation rows on, linear() on fp32 activations runs the prefill
-// GEMM (split activations, fp16 MFMA) instead of the decode GEMVs.
-// Measured (MI355X, graph replay): the fp32 GEMM overtakes the batched GEMV (one pass
-// over W per 16 rows) at 64-96 rows on 11008-row weights, at 96-128 on 4096-row and
-// 28672 x 8192 weights; from 128 rows it is ahead or even on every BASELINE shape.
+// GEMM (split activations, fp16 MFMA) instead of the decode GEMVs: 128, or 64 on
+// weights of at least 10240 rows, whose 64 x 64 tiles fill 160+ CUs from 64 rows.
+// Measured (MI355X, graph replay, µs at 48 / 64 / 96 / 128 rows, batched GEMV passes
+// of 16 rows vs fp32 GEMM): Q4_0 11008 x 4096 39.7 / 51.2 / 77.3 / 102 vs 46.6 / 46.8 /
+// 55.4 / 56.0, Q8_0 44.7 / 57.6 / 88.9 / 112 vs 46.2 / 46.3 / 53.8 / 56.6, Q4_0
+// 28672 x 8192 129 / 165 / 231 / 303 vs 121 / 123 / 201 / 201; with fewer weight rows
+// the GEMM's grid stays small and the GEMV keeps its lead longer: 4096 x 11008 69 / 102
+// / 134 vs 111 at 64 / 96 / 128, 1024 x 8192 39 / 58 / 77 vs 71-73, 4096 x 4096 36 /
+// 54 vs 39 / 40 at 64 / 96.
 constexpr int64_t kGemmMinRows = 128;
+constexpr int64_t kGemmMinRowsWide = 64;
+constexpr int64_t kGemmWideRows = 10240;
+inline int64_t gemm_min_rows(int64_t n_rows) { return n_rows >= kGemmWideRows ? kGemmMinRowsWide : kGemmMinRows; }
 
 // IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {

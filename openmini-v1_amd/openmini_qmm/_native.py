@@ -90,6 +90,7 @@ SIGNATURES = {
     "openmini_qmm_gemm_bf16": (_i, [_p, _p, _p, _i64, _p]),
     "openmini_qmm_gemm_f32_workspace_bytes": (_sz, [_i64, _i64]),
     "openmini_qmm_gemm_launch_shape": (_i, [_p, _i64, _i]),
+    "openmini_qmm_gemm_min_rows": (_i64, [_p]),
     "openmini_qmm_gemm_f32": (_i, [_p, _p, _p, _i64, _p, _sz, _p]),
     "openmini_qmm_gemv_multi": (_i, [ctypes.POINTER(_p), _i, _p, ctypes.POINTER(_p), _i64, _p]),
     "openmini_qmm_ffn_gate_up": (_i, [_p, _p, _p, _p, _i64, _p]),

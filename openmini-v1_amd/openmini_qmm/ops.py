@@ -216,10 +216,19 @@ class QuantizedWeight:
         self.n_rows, self.k_cols = int(n_rows), int(k_cols)
         return self
 
+    def gemm_min_rows(self) -> int:
+        """The fewest activation rows from which linear() runs the fp32 prefill GEMM on
+        this weight (openmini_qmm_gemm_min_rows): GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE on
+        weights of GEMM_WIDE_ROWS+ rows, 0 for the block-minimum types (never)."""
+        t = lib().openmini_qmm_gemm_min_rows(self.handle)
+        check(t if t < 0 else 0)
+        return int(t)
+
     def prefill_gemm(self, m: int) -> bool:
         """Whether linear() on m rows of this weight runs the fp32 prefill GEMM (the
-        library's rule: from GEMM_MIN_ROWS rows, types without a block minimum)."""
-        return m >= GEMM_MIN_ROWS and int(self.tensor_type) not in (GgufTensorType.Q4_1, GgufTensorType.Q5K)
+        library's rule, asked of the library)."""
+        t = self.gemm_min_rows()
+        return t > 0 and m >= t
 
     def info(self) -> _native.WeightInfo:
         info = _native.WeightInfo()
@@ -275,8 +284,12 @@ def gemm_f32_workspace(m: int, k_cols: int) -> DeviceBuffer:
 
 
 # Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
-# (the library's own threshold for openmini_qmm_linear_host).
+# (the library's own threshold for openmini_qmm_linear_host): GEMM_MIN_ROWS, and
+# GEMM_MIN_ROWS_WIDE on weights of at least GEMM_WIDE_ROWS rows.  Per weight:
+# QuantizedWeight.gemm_min_rows().
 GEMM_MIN_ROWS = 128
+GEMM_MIN_ROWS_WIDE = 64
+GEMM_WIDE_ROWS = 10240
 
 
 # ---- quant_simd safe API (validated dequantization) on the GPU ----------------------
@@ -453,7 +466,8 @@ class HipQuantGemmEngine:
                         bias=None) -> np.ndarray:
         """FFNWeights::forward's hidden state silu(x . Wg^T) * (x . Wu^T) (+ bias)
         (model.rs:728-731): gate and up in one launch (openmini_qmm_ffn_gate_up), or from
-        GEMM_MIN_ROWS rows on the fp32 prefill GEMMs (openmini_qmm_ffn_gate_up_f32).  The
+        the gate weight's gemm_min_rows() rows on the fp32 prefill GEMMs
+        (openmini_qmm_ffn_gate_up_f32).  The
         ndarray fallback's fused_gemm_silu (gemm_engine.rs:112-130) computes
         gate * silu(up) on untransposed weights instead; that branch is not followed."""
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -45,10 +45,13 @@ impl HipQuantWeight {
         Ok(Self { raw, n: n_rows, k: k_cols, tensor_type: t as i32 })
     }
 
-    /// Whether linear() on `m` rows of this weight runs the fp32 prefill GEMM (the
-    /// library's rule: from GEMM_MIN_ROWS rows, types without a block minimum).
+    /// Whether linear() on `m` rows of this weight runs the fp32 prefill GEMM, asked of
+    /// the library (openmini_qmm_gemm_min_rows: GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE on
+    /// weights of GEMM_WIDE_ROWS+ rows, 0 = never for the block-minimum types; a failed
+    /// query answers no and the GEMV call that follows reports the error).
     pub fn prefill_gemm(&self, m: usize) -> bool {
-        m >= GEMM_MIN_ROWS && self.tensor_type != 3 && self.tensor_type != 13
+        let t = unsafe { ffi::openmini_qmm_gemm_min_rows(self.raw) };
+        t > 0 && m as i64 >= t
     }
 
     pub fn info(&self) -> Result<ffi::WeightInfo, String> {
@@ -97,8 +100,12 @@ pub trait QuantGemmEngine: Send + Sync {
 pub struct HipQuantGemmEngine;
 
 /// Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
-/// (openmini_qmm_linear_host makes the same choice).
+/// (openmini_qmm_linear_host makes the same choice): GEMM_MIN_ROWS, and
+/// GEMM_MIN_ROWS_WIDE on weights of at least GEMM_WIDE_ROWS rows.  Per weight:
+/// HipQuantWeight::prefill_gemm.
 pub const GEMM_MIN_ROWS: usize = 128;
+pub const GEMM_MIN_ROWS_WIDE: usize = 64;
+pub const GEMM_WIDE_ROWS: usize = 10240;
 
 fn gen_err(e: String) -> InferenceError {
     InferenceError::generation(e)

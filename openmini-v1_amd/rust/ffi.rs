@@ -103,6 +103,7 @@ extern "C" {
     pub fn openmini_qmm_gemm_bf16(weight: *const QWeight, d_x: *const u16, d_y: *mut f32, m: i64, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_gemm_f32_workspace_bytes(m: i64, k_cols: i64) -> usize;
     pub fn openmini_qmm_gemm_launch_shape(weight: *const QWeight, m: i64, split_x: c_int) -> c_int;
+    pub fn openmini_qmm_gemm_min_rows(weight: *const QWeight) -> i64;
     pub fn openmini_qmm_gemm_f32(weight: *const QWeight, d_x: *const f32, d_y: *mut f32, m: i64, d_work: *mut c_void, work_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_gemv_multi(weights: *const *const QWeight, count: c_int, d_x: *const f32, d_ys: *const *mut f32, batch: i64, stream: *mut c_void) -> c_int;
     pub fn openmini_qmm_ffn_gate_up(gate: *const QWeight, up: *const QWeight, d_x: *const f32, d_h: *mut f32, batch: i64, stream: *mut c_void) -> c_int;

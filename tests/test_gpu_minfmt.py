@@ -127,7 +127,7 @@ def test_minfmt_prefill_rows_run_the_gemv(qmm, orc, qtype):
     _native.check(L.openmini_qmm_linear_host(w.handle, x.ctypes.data_as(ctypes.c_void_p),
                                              y.ctypes.data_as(ctypes.c_void_p), m))
     assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x), TOL, f"type={qtype} m={m}")
-    assert w.prefill_gemm(m) is False
+    assert w.prefill_gemm(m) is False and w.gemm_min_rows() == 0
     dx = qmm.DeviceBuffer.from_numpy(x)
     dy = qmm.DeviceBuffer(m * N * 4)
     work = qmm.gemm_f32_workspace(m, K)
