@@ -596,8 +596,8 @@ hipError_t launch_shape(const Weight& w, const uint16_t* x, const int* x_exp, fl
 // its own and picks the fastest in 39 of 40 (worst +0.6%).  Fixed per shape, so a
 // row's bits depend only on m and the weight.  A shape with per_cu < 0 is not built
 // for the instance: Q6_K on bf16 x has no 128 x 96 tiles (its super-block sums take
-// 96 more registers and would spill), and split x no 64 x 96 tiles (64 x 64 ran as
-// fast or faster at every measured size).
+// 96 more registers and would spill), and split x no 64 x 96 tiles (64 x 64 ran
+// faster or within 0.6% at every measured size).
 int choose_shape(const Weight& w, int64_t m, const int (&per_cu)[4], bool split_x) {
     static const int bm[4] = {128, 128, 64, 64}, wt[4] = {3, 2, 3, 2};
     static const double cost_per_flop[2][4] = {{1.00, 1.10, 1.25, 1.35},   // bf16 x
