@@ -479,7 +479,9 @@ hipError_t run(const GemvGroup& grp, int64_t groups, int64_t k, const float* x, 
 // (two workgroups per CU or fewer) with K of 64+ groups: 16 waves of 2-group phases,
 // twice the waves in flight (two interleaved passes, Q4_0: 4096 x 11008 7.25-7.58 ->
 // 7.03-7.14 us, 8192 x 28672 26.7-27.3 -> 25.5-25.6, 8192 x 8192 8.40-8.51 ->
-// 8.31-8.36; Q8_0 4096 x 11008 lost 10% and 4096 x 4096 (32 groups) gained nothing).
+// 8.31-8.36; Q8_0 4096 x 11008 lost 10% and 4096 x 4096 (32 groups) gained nothing;
+// Q6_K 4096 x 11008 9.0-9.1 -> 9.4-9.5, 8192 x 8192 11.5 -> 13.7-13.9, Q5_K 4096 x 11008
+// 9.4 -> 10.4-10.5).
 // Fewer, longer waves lose at the headline shape: 11008 x 4096 Q4_0 W = 8 6.29-6.33
 // us, W = 4 (8-group phases) 6.64-6.67, W = 2 8.02-8.10.
 // More batch rows: at most 8 (LDS and registers per wave grow with the batch).  Short
