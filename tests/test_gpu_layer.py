@@ -144,6 +144,25 @@ def test_layer_prefill_rows(qmm, orc):
     assert_parity(attn.project_o(x), orc.linear_f64(Q8_0, ws[3][1], H, H, x), TOL, "o_proj")
 
 
+@pytest.mark.parametrize("M", [64, 100])
+def test_layer_mixed_routing(qmm, orc, M):
+    """Gate / up of 10240+ rows take the fp32 GEMM from GEMM_MIN_ROWS_WIDE rows, the
+    narrower down projection keeps the decode GEMVs below GEMM_MIN_ROWS: between the
+    two, FFNWeights.forward runs the GEMM pair and then the down GEMV on its hidden
+    state, and both halves meet the oracle."""
+    H, I = 512, qmm.GEMM_WIDE_ROWS
+    print(f"layer mixed routing M={M}", flush=True)
+    (wg, bg), (wu, bu), (wd, bd) = _weights(qmm, Q4_0, ((I, H), (I, H), (H, I)), seed=0x9660)
+    assert wg.prefill_gemm(M) and not wd.prefill_gemm(M)
+    ffn = qmm.FFNWeights(wg, wu, wd)
+    x = synth.normal(0x9661 + M, (M, H), 1.0)
+    h = ffn.hidden(x)
+    assert_parity(h, orc.ffn_hidden_f64(Q4_0, bg, bu, I, H, x), TOL, "hidden")
+    out = ffn.forward(x)
+    assert np.all(np.isfinite(out))
+    assert_parity(out, orc.linear_f64(Q4_0, bd, H, I, h), TOL, "down")
+
+
 def test_ffn_gate_up_rejects_mismatched_pair(qmm):
     (wg, _), (wu, _) = _weights(qmm, Q4_0, ((64, 128), (48, 128)), seed=0x9700)
     dx, dh = qmm.DeviceBuffer(128 * 4), qmm.DeviceBuffer(64 * 4)
