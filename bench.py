@@ -637,6 +637,21 @@ def main(argv=None) -> int:
                         "launch_shape": r["launch_shape"], "sha256": r["sha256"]})
         log(f"q8_0 gemm M=512 f32 x: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s "
             f"({r['kernel_ms'] / gemm['kernel_ms']:.2f}x the bf16 leg)")
+        # a short prompt on the FFN up shape: linear() on 96 fp32 rows takes the fp32 GEMM
+        # on weights of 10240+ rows (openmini_qmm_gemm_min_rows), timed beside the
+        # batched-GEMV passes of 16 rows it ran before
+        m_short = 96
+        rl = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), M=m_short, f32_x=True)
+        gl = bench_gemv(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), N=11008, K=4096,
+                       qtype=Q8_0, batch=m_short, seed=0x5EED0003)
+        prefill.append({"workload": f"q8_0_linear_n11008_k4096_m{m_short}_f32x", "unit": "TFLOP/s",
+                        "value": round(rl["tflops_kernel"], 2), "kernel_us": round(rl["kernel_ms"] * 1e3, 3),
+                        "frac": round(rl["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
+                        "route": "fp32 GEMM (openmini_qmm_gemm_min_rows = 64 on this weight)",
+                        "gemv_passes_us": round(gl["kernel_ms"] * 1e3, 3),
+                        "launch_shape": rl["launch_shape"], "sha256": rl["sha256"]})
+        log(f"q8_0 linear M={m_short} f32 x: GEMM {rl['kernel_ms'] * 1e3:.2f} us vs GEMV passes "
+            f"{gl['kernel_ms'] * 1e3:.2f} us")
     layer = None
     if not args.no_layer:
         layer = bench_layer(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4))
