@@ -638,7 +638,7 @@ def main(argv=None) -> int:
         log(f"q8_0 gemm M=512 f32 x: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s "
             f"({r['kernel_ms'] / gemm['kernel_ms']:.2f}x the bf16 leg)")
         # a short prompt on the FFN up shape: linear() on 96 fp32 rows takes the fp32 GEMM
-        # on weights of 10240+ rows (openmini_qmm_gemm_min_rows), timed beside the
+        # here (openmini_qmm_gemm_min_rows = 64 on this weight), timed beside the
         # batched-GEMV passes of 16 rows it ran before
         m_short = 96
         rl = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), M=m_short, f32_x=True)

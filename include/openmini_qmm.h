@@ -229,10 +229,12 @@ int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, 
 
 /* Routing query, no counterpart in the reference: the fewest activation rows from which
  * openmini_qmm_linear_host (and _noalloc) run the fp32 prefill GEMM on this weight
- * rather than the decode GEMVs: 128, or 64 on weights of at least 10240 rows (N), where
- * the GEMM's grid fills the CUs from 64 rows; 0 for Q4_1 / Q5_K, which have no prefill
- * GEMM.  Engines that call the GEMM and GEMV entry points themselves use it to make the
- * same choice.  A negative status on error. */
+ * rather than the decode GEMVs: the first m in [64, 128) where the GEMM's estimated
+ * time (about 10 ns per K element while its grid fits one round) beats the GEMVs' (one
+ * pass per 16 rows, about 6.5 us plus the weight bytes at 3 TB/s), else 128; 0 for
+ * Q4_1 / Q5_K, which have no prefill GEMM.  Depends on the weight's type and shape
+ * only.  Engines that call the GEMM and GEMV entry points themselves use it to make
+ * the same choice.  A negative status on error. */
 int64_t openmini_qmm_gemm_min_rows(const openmini_qweight_t* weight);
 int openmini_qmm_gemm_f32(const openmini_qweight_t* weight, const float* d_x, float* d_y, int64_t m,
                           void* d_work, size_t work_bytes, void* stream);
@@ -269,8 +271,8 @@ int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_
                                  void* stream);
 
 /* GemmEngine::matmul-shaped convenience on host memory: y[m, N] = x[m, K] . W^T,
- * fp32 in/out, synchronous.  Below openmini_qmm_gemm_min_rows rows (128; 64 on weights
- * of 10240+ rows) the decode GEMVs, from there on the fp32 prefill GEMM
+ * fp32 in/out, synchronous.  Below openmini_qmm_gemm_min_rows rows (64-128, by the
+ * weight's shape) the decode GEMVs, from there on the fp32 prefill GEMM
  * (openmini_qmm_gemm_f32; Q4_1 / Q5_K weights: the batched GEMV at any row count); x,
  * y and the GEMM's workspace are allocated per call. */
 int openmini_qmm_linear_host(const openmini_qweight_t* weight, const float* x, float* y,

@@ -86,7 +86,9 @@ int check_gemm_type(const qmm::Weight& w) {
     return OPENMINI_QMM_OK;
 }
 // Rows that linear() hands to the fp32 prefill GEMM rather than the decode GEMVs.
-bool gemm_rows(const qmm::Weight& w, int64_t m) { return m >= qmm::gemm_min_rows(w.n) && !qmm::has_block_min(w.type); }
+bool gemm_rows(const qmm::Weight& w, int64_t m) {
+    return !qmm::has_block_min(w.type) && m >= qmm::gemm_min_rows(w.type, w.n, w.k);
+}
 bool plain_type(int type) { return type == OPENMINI_QMM_Q4_0 || type == OPENMINI_QMM_Q8_0; }
 // quant_simd::safe_dequantize's types (quant_simd.rs:284-302, F16/F32 aside).
 bool safe_type(int type) {
@@ -519,7 +521,8 @@ int openmini_qmm_gemm_bf16(const openmini_qweight_t* weight, const uint16_t* d_x
 int64_t openmini_qmm_gemm_min_rows(const openmini_qweight_t* weight) {
     const int rc = check_weight(weight);
     if (rc != OPENMINI_QMM_OK) return rc;
-    return qmm::has_block_min(weight->w.type) ? 0 : qmm::gemm_min_rows(weight->w.n);
+    const qmm::Weight& w = weight->w;
+    return qmm::has_block_min(w.type) ? 0 : qmm::gemm_min_rows(w.type, w.n, w.k);
 }
 
 int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, int split_x) {
@@ -659,7 +662,7 @@ int openmini_qmm_ffn_gate_up_f32(const openmini_qweight_t* gate, const openmini_
 }
 
 namespace {
-// linear(x, W) on device buffers: the decode GEMVs below qmm::gemm_min_rows(N) rows (and for
+// linear(x, W) on device buffers: the decode GEMVs below qmm::gemm_min_rows rows (and for
 // block-minimum types at any count), else the fp32-activation prefill GEMM (its
 // workspace at d_work).
 hipError_t linear_rows(const qmm::Weight& w, const float* dx, float* dy, int64_t m, void* d_work) {

@@ -83,20 +83,10 @@ constexpr int kQK = 32;
 constexpr int kMaxGemvBatch = 4;  // batch rows per launch of the single-row-tuned GEMV
 constexpr int kBatchRows = 16;    // batch rows per launch of the batched GEMV (its MFMA rows)
 constexpr int kMaxGroup = 4;      // weights sharing one GEMV launch
-// From this many activation rows on, linear() on fp32 activations runs the prefill
-// GEMM (split activations, fp16 MFMA) instead of the decode GEMVs: 128, or 64 on
-// weights of at least 10240 rows, whose 64 x 64 tiles fill 160+ CUs from 64 rows.
-// Measured (MI355X, graph replay, µs at 48 / 64 / 96 / 128 rows, batched GEMV passes
-// of 16 rows vs fp32 GEMM): Q4_0 11008 x 4096 39.7 / 51.2 / 77.3 / 102 vs 46.6 / 46.8 /
-// 55.4 / 56.0, Q8_0 44.7 / 57.6 / 88.9 / 112 vs 46.2 / 46.3 / 53.8 / 56.6, Q4_0
-// 28672 x 8192 129 / 165 / 231 / 303 vs 121 / 123 / 201 / 201; with fewer weight rows
-// the GEMM's grid stays small and the GEMV keeps its lead longer: 4096 x 11008 69 / 102
-// / 134 vs 111 at 64 / 96 / 128, 1024 x 8192 39 / 58 / 77 vs 71-73, 4096 x 4096 36 /
-// 54 vs 39 / 40 at 64 / 96.
+// linear() on fp32 activations runs the prefill GEMM (split activations, fp16 MFMA)
+// from 128 rows on for every weight it takes (gemm_min_rows may choose earlier).
 constexpr int64_t kGemmMinRows = 128;
-constexpr int64_t kGemmMinRowsWide = 64;
-constexpr int64_t kGemmWideRows = 10240;
-inline int64_t gemm_min_rows(int64_t n_rows) { return n_rows >= kGemmWideRows ? kGemmMinRowsWide : kGemmMinRows; }
+constexpr int64_t kGemmMinRowsLow = 64;  // gemm_min_rows never chooses below this
 
 // IEEE binary16 bits -> binary32 (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
@@ -127,6 +117,27 @@ inline int bytes_per_block(int type) {
 // Q8_0 blocks that share one d, so Q8_K weights become Q8_0 chunks and run every Q8_0
 // kernel with the same values.
 inline int chunk_type(int type) { return type == OPENMINI_QMM_Q8_K ? OPENMINI_QMM_Q8_0 : type; }
+
+// The fewest activation rows from which linear() takes the fp32 GEMM on a weight of
+// n_rows x k_cols: the first m in [64, 128) where the GEMM's estimated time beats the
+// decode GEMVs', else 128.  Estimates (MI355X, graph replay): the GEMM on a grid of at
+// most one round takes about 10 ns per K element (its workgroups walk K serially:
+// K = 3072 / 4096 / 8192 / 11008 / 13824 -> 31 / 39-46 / 82-90 / 110 / 137 us at
+// 64-128 rows), a round being 512 workgroups of 64 x 64; the batched GEMV runs one
+// pass per 16 rows of about 6.5 us plus the weight bytes at 3 TB/s.  Over 18 weight
+// shapes x 48-112 rows (Q4_0 / Q8_0 / Q4_K / Q6_K, 1024-28672 rows, K 3072-13824) the
+// choice loses at most 17% against the faster path (Q8_0 4096 x 11008 at 80 rows), a
+// fixed 128 up to 85% (3072 x 3072 at 112 rows: GEMV 60.0 vs GEMM 32.4 us).
+inline int64_t gemm_min_rows(int type, int64_t n_rows, int64_t k_cols) {
+    const double w_bytes = (double)n_rows * (double)k_cols * bytes_per_block(type) / weight_block_elems(type);
+    const double pass_us = 6.5 + w_bytes / 3.0e6;
+    for (int64_t m = kGemmMinRowsLow; m < kGemmMinRows; ++m) {
+        const int64_t wgs = (n_rows + 63) / 64 * ((m + 63) / 64);
+        const double gemm_us = 0.010 * (double)k_cols * (double)((wgs + 511) / 512);
+        if (gemm_us < (double)((m + 15) / 16) * pass_us) return m;
+    }
+    return kGemmMinRows;
+}
 
 // GgufTensorType::{block_size, bytes_per_block} (src/model/inference/gguf.rs:348-379)
 // for the layouts the dequantization entry points accept; 0 for others.

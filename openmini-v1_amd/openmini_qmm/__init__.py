@@ -7,7 +7,7 @@ operator interface (see ops.py) plus synthetic-input helpers (synth.py).
 from ._native import LIB_PATH, Q4_0, Q8_0, QmmError, lib  # noqa: F401
 from .layer import (AttentionWeights, FFNWeights, ffn_gate_up, ffn_gate_up_bf16,  # noqa: F401
                     ffn_gate_up_f32, gemv_multi)
-from .ops import (GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE, GEMM_WIDE_ROWS, DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,  # noqa: F401
+from .ops import (GEMM_MIN_ROWS, GEMM_MIN_ROWS_LOW, DeviceBuffer, GgufTensorType, HipQuantGemmEngine, HipQuantOps,  # noqa: F401
                   InsufficientData, InvalidInput, QuantError, QuantizedWeight, Stream,
                   UnsupportedType, convert_to_soa_layout, dequantize, dequantize_simd,
                   get_gemm_engine, init, linear,

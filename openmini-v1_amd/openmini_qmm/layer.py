@@ -11,8 +11,8 @@ several linear layers on one input:
     itself are not part of the quantized linear layer.
 
 The host-array methods are synchronous and mirror the reference's signatures; from
-the weight's gemm_min_rows() rows on (prefill: GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE on
-weights of GEMM_WIDE_ROWS+ rows) they run the fp32-activation GEMMs, below it (and for
+the weight's gemm_min_rows() rows on (prefill: 64-128 rows by the weight's shape)
+they run the fp32-activation GEMMs, below it (and for
 Q4_1 / Q5_K weights, whose blocks carry a minimum) the decode GEMVs.  The *_device methods take device buffers and a stream and only enqueue
 work.
 """

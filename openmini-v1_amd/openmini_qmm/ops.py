@@ -218,8 +218,8 @@ class QuantizedWeight:
 
     def gemm_min_rows(self) -> int:
         """The fewest activation rows from which linear() runs the fp32 prefill GEMM on
-        this weight (openmini_qmm_gemm_min_rows): GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE on
-        weights of GEMM_WIDE_ROWS+ rows, 0 for the block-minimum types (never)."""
+        this weight (openmini_qmm_gemm_min_rows): between GEMM_MIN_ROWS_LOW and
+        GEMM_MIN_ROWS by the weight's shape, 0 for the block-minimum types (never)."""
         t = lib().openmini_qmm_gemm_min_rows(self.handle)
         check(t if t < 0 else 0)
         return int(t)
@@ -284,12 +284,10 @@ def gemm_f32_workspace(m: int, k_cols: int) -> DeviceBuffer:
 
 
 # Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
-# (the library's own threshold for openmini_qmm_linear_host): GEMM_MIN_ROWS, and
-# GEMM_MIN_ROWS_WIDE on weights of at least GEMM_WIDE_ROWS rows.  Per weight:
-# QuantizedWeight.gemm_min_rows().
+# (the library's own threshold for openmini_qmm_linear_host): per weight,
+# QuantizedWeight.gemm_min_rows(), between GEMM_MIN_ROWS_LOW and GEMM_MIN_ROWS.
 GEMM_MIN_ROWS = 128
-GEMM_MIN_ROWS_WIDE = 64
-GEMM_WIDE_ROWS = 10240
+GEMM_MIN_ROWS_LOW = 64
 
 
 # ---- quant_simd safe API (validated dequantization) on the GPU ----------------------

@@ -46,9 +46,9 @@ impl HipQuantWeight {
     }
 
     /// Whether linear() on `m` rows of this weight runs the fp32 prefill GEMM, asked of
-    /// the library (openmini_qmm_gemm_min_rows: GEMM_MIN_ROWS, GEMM_MIN_ROWS_WIDE on
-    /// weights of GEMM_WIDE_ROWS+ rows, 0 = never for the block-minimum types; a failed
-    /// query answers no and the GEMV call that follows reports the error).
+    /// the library (openmini_qmm_gemm_min_rows: between GEMM_MIN_ROWS_LOW and
+    /// GEMM_MIN_ROWS by the weight's shape, 0 = never for the block-minimum types; a
+    /// failed query answers no and the GEMV call that follows reports the error).
     pub fn prefill_gemm(&self, m: usize) -> bool {
         let t = unsafe { ffi::openmini_qmm_gemm_min_rows(self.raw) };
         t > 0 && m as i64 >= t
@@ -100,12 +100,10 @@ pub trait QuantGemmEngine: Send + Sync {
 pub struct HipQuantGemmEngine;
 
 /// Rows from which the host calls run the fp32 prefill GEMM instead of the decode GEMVs
-/// (openmini_qmm_linear_host makes the same choice): GEMM_MIN_ROWS, and
-/// GEMM_MIN_ROWS_WIDE on weights of at least GEMM_WIDE_ROWS rows.  Per weight:
-/// HipQuantWeight::prefill_gemm.
+/// (openmini_qmm_linear_host makes the same choice): per weight,
+/// HipQuantWeight::prefill_gemm, between GEMM_MIN_ROWS_LOW and GEMM_MIN_ROWS.
 pub const GEMM_MIN_ROWS: usize = 128;
-pub const GEMM_MIN_ROWS_WIDE: usize = 64;
-pub const GEMM_WIDE_ROWS: usize = 10240;
+pub const GEMM_MIN_ROWS_LOW: usize = 64;
 
 fn gen_err(e: String) -> InferenceError {
     InferenceError::generation(e)

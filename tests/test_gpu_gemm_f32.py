@@ -159,18 +159,23 @@ def test_gemm_f32_repeatable_and_row_independent(qmm):
     assert np.array_equal(y[:150].view(np.uint32), y2[:150].view(np.uint32))
 
 
-@pytest.mark.parametrize("N,K", [(1100, 4096), (10240, 1024)])
+@pytest.mark.parametrize("N,K", [(1100, 4096), (10240, 1024), (1024, 8192)])
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_linear_host_routes_prefill_to_gemm(qmm, orc, qtype, N, K):
     """openmini_qmm_linear_host (GemmEngine::matmul's binding) runs the decode GEMVs below
-    the weight's openmini_qmm_gemm_min_rows (GEMM_MIN_ROWS; GEMM_MIN_ROWS_WIDE from
-    GEMM_WIDE_ROWS weight rows) and the fp32 GEMM from there on: one row below the
-    threshold it equals openmini_qmm_gemv, at the threshold and at 300 rows
-    openmini_qmm_gemm_f32, bit for bit, and both meet the oracle."""
+    the weight's openmini_qmm_gemm_min_rows (64-128 by the weight's shape) and the fp32
+    GEMM from there on: one row below the threshold it equals openmini_qmm_gemv, at the
+    threshold and at 300 rows openmini_qmm_gemm_f32, bit for bit, and both meet the
+    oracle.  A short-K weight of many rows switches at the lowest count, a long-K
+    weight of few rows (whose GEMM grid stays small) at the highest."""
     blocks = synth.weight_blocks(qtype, N, K, seed=0xF40 + qtype)
     w = qmm.QuantizedWeight(qtype, blocks, N, K)
     t = w.gemm_min_rows()
-    assert t == (qmm.GEMM_MIN_ROWS_WIDE if N >= qmm.GEMM_WIDE_ROWS else qmm.GEMM_MIN_ROWS)
+    assert qmm.GEMM_MIN_ROWS_LOW <= t <= qmm.GEMM_MIN_ROWS
+    if (N, K) == (10240, 1024):
+        assert t == qmm.GEMM_MIN_ROWS_LOW
+    if (N, K) == (1024, 8192):
+        assert t == qmm.GEMM_MIN_ROWS
     assert not w.prefill_gemm(t - 1) and w.prefill_gemm(t)
     for M in (t - 1, t, 300):
         print(f"linear_host route type={qtype} N={N} K={K} M={M}", flush=True)

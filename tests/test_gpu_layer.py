@@ -146,11 +146,11 @@ def test_layer_prefill_rows(qmm, orc):
 
 @pytest.mark.parametrize("M", [64, 100])
 def test_layer_mixed_routing(qmm, orc, M):
-    """Gate / up of 10240+ rows take the fp32 GEMM from GEMM_MIN_ROWS_WIDE rows, the
-    narrower down projection keeps the decode GEMVs below GEMM_MIN_ROWS: between the
-    two, FFNWeights.forward runs the GEMM pair and then the down GEMV on its hidden
-    state, and both halves meet the oracle."""
-    H, I = 512, qmm.GEMM_WIDE_ROWS
+    """Gate / up of 10240 rows over a short K take the fp32 GEMM from GEMM_MIN_ROWS_LOW
+    rows, the down projection (few rows, long K) keeps the decode GEMVs below
+    GEMM_MIN_ROWS: between the two, FFNWeights.forward runs the GEMM pair and then the
+    down GEMV on its hidden state, and both halves meet the oracle."""
+    H, I = 512, 10240
     print(f"layer mixed routing M={M}", flush=True)
     (wg, bg), (wu, bu), (wd, bd) = _weights(qmm, Q4_0, ((I, H), (I, H), (H, I)), seed=0x9660)
     assert wg.prefill_gemm(M) and not wd.prefill_gemm(M)

@@ -46,13 +46,13 @@ def test_noalloc_matches_linear_host(qmm, orc, qtype):
         assert_parity(y, orc.linear_f64(qtype, blocks, N, K, x), TOL, f"N={N} K={K} m={m}")
 
 
-def _staged_bytes(qmm, rows, N, K):
-    """The staging the entry point needs for `rows` rows: x, from GEMM_MIN_ROWS rows on
-    the fp32 GEMM's workspace (split x and one exponent per row), then y, each from a
-    256-byte boundary."""
+def _staged_bytes(rows, N, K, t):
+    """The staging the entry point needs for `rows` rows: x, from the weight's
+    gemm_min_rows() = t rows on the fp32 GEMM's workspace (split x and one exponent per
+    row), then y, each from a 256-byte boundary."""
     def up(v):
         return (v + 255) // 256 * 256
-    work = up(rows * K * 4) + rows * 4 if rows >= qmm.GEMM_MIN_ROWS else 0
+    work = up(rows * K * 4) + rows * 4 if rows >= t else 0
     return up(rows * K * 4) + work + rows * N * 4
 
 
@@ -61,8 +61,9 @@ def test_noalloc_rejects_past_staging(qmm):
     N, K = 8192, 8192
     blocks = synth.weight_blocks(Q4_0, N, K, seed=0xA30)
     w = qmm.QuantizedWeight(Q4_0, blocks, N, K)
-    rows_max = max(r for r in range(1, 600) if _staged_bytes(qmm, r, N, K) <= 16 << 20)
-    assert rows_max >= qmm.GEMM_MIN_ROWS  # the largest call runs the fp32 GEMM
+    t = w.gemm_min_rows()
+    rows_max = max(r for r in range(1, 600) if _staged_bytes(r, N, K, t) <= 16 << 20)
+    assert rows_max >= t  # the largest call runs the fp32 GEMM
     m = rows_max + 1
     x = np.zeros((m, K), np.float32)
     y = np.full((m, N), 7.0, np.float32)
