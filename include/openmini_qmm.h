@@ -231,7 +231,7 @@ int openmini_qmm_gemm_launch_shape(const openmini_qweight_t* weight, int64_t m, 
  * openmini_qmm_linear_host (and _noalloc) run the fp32 prefill GEMM on this weight
  * rather than the decode GEMVs: the first m in [64, 128) where the GEMM's estimated
  * time (about 10 ns per K element while its grid fits one round) beats the GEMVs' (one
- * pass per 16 rows, about 6.5 us plus the weight bytes at 3 TB/s), else 128; 0 for
+ * pass per 16 rows, about 6.5 us plus the weight bytes at 3-5 TB/s), else 128; 0 for
  * Q4_1 / Q5_K, which have no prefill GEMM.  Depends on the weight's type and shape
  * only.  Engines that call the GEMM and GEMV entry points themselves use it to make
  * the same choice.  A negative status on error. */

@@ -124,13 +124,14 @@ inline int chunk_type(int type) { return type == OPENMINI_QMM_Q8_K ? OPENMINI_QM
 // most one round takes about 10 ns per K element (its workgroups walk K serially:
 // K = 3072 / 4096 / 8192 / 11008 / 13824 -> 31 / 39-46 / 82-90 / 110 / 137 us at
 // 64-128 rows), a round being 512 workgroups of 64 x 64; the batched GEMV runs one
-// pass per 16 rows of about 6.5 us plus the weight bytes at 3 TB/s.  Over 18 weight
-// shapes x 48-112 rows (Q4_0 / Q8_0 / Q4_K / Q6_K, 1024-28672 rows, K 3072-13824) the
-// choice loses at most 17% against the faster path (Q8_0 4096 x 11008 at 80 rows), a
-// fixed 128 up to 85% (3072 x 3072 at 112 rows: GEMV 60.0 vs GEMM 32.4 us).
+// pass per 16 rows of about 6.5 us plus the weight bytes at 5 TB/s (Q8_0 chunks) or
+// 3 TB/s (the others).  Over 18 weight shapes x 48-112 rows (Q4_0 / Q8_0 / Q4_K /
+// Q6_K, 1024-28672 rows, K 3072-13824) the choice loses at most 9% against the faster
+// path (Q4_0 2048 x 4096 at 80 rows), a fixed 128 up to 85% (3072 x 3072 at 112 rows:
+// GEMV 60.0 vs GEMM 32.4 us).
 inline int64_t gemm_min_rows(int type, int64_t n_rows, int64_t k_cols) {
     const double w_bytes = (double)n_rows * (double)k_cols * bytes_per_block(type) / weight_block_elems(type);
-    const double pass_us = 6.5 + w_bytes / 3.0e6;
+    const double pass_us = 6.5 + w_bytes / (type == OPENMINI_QMM_Q8_0 ? 5.0e6 : 3.0e6);
     for (int64_t m = kGemmMinRowsLow; m < kGemmMinRows; ++m) {
         const int64_t wgs = (n_rows + 63) / 64 * ((m + 63) / 64);
         const double gemm_us = 0.010 * (double)k_cols * (double)((wgs + 511) / 512);
