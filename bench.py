@@ -168,6 +168,7 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
     work = qmm.gemm_f32_workspace(M, K) if f32_x else None
     sh = stream.handle
     shape = _native.lib().openmini_qmm_gemm_launch_shape(ws[0].handle, M, int(f32_x))
+    min_rows = int(_native.lib().openmini_qmm_gemm_min_rows(ws[0].handle))
 
     def launch(i):
         if f32_x:
@@ -184,7 +185,7 @@ def bench_gemm(qmm, hipr, stream, steps, warmup, N=11008, K=4096, M=512, qtype=Q
     for w in ws:
         w.close()
     return {
-        "N": N, "K": K, "M": M, "weight_copies": copies, "launch_shape": shape,
+        "N": N, "K": K, "M": M, "weight_copies": copies, "launch_shape": shape, "gemm_min_rows": min_rows,
         "sha256": {"weight": sha256(blocks), ("x_f32" if f32_x else "x_bf16"): sha256(x32 if f32_x else xb)},
         "ms_per_step": total_ms / steps, "kernel_ms": per_launch_ms,
         "tflops_wall": flops * steps / (total_ms * 1e-3) / 1e12,
@@ -638,8 +639,8 @@ def main(argv=None) -> int:
         log(f"q8_0 gemm M=512 f32 x: {r['kernel_ms'] * 1e3:.2f} us, {r['tflops_kernel']:.1f} TFLOP/s "
             f"({r['kernel_ms'] / gemm['kernel_ms']:.2f}x the bf16 leg)")
         # a short prompt on the FFN up shape: linear() on 96 fp32 rows takes the fp32 GEMM
-        # here (openmini_qmm_gemm_min_rows = 64 on this weight), timed beside the
-        # batched-GEMV passes of 16 rows it ran before
+        # here (from openmini_qmm_gemm_min_rows rows on), timed beside the batched-GEMV
+        # passes of 16 rows it ran before
         m_short = 96
         rl = bench_gemm(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), M=m_short, f32_x=True)
         gl = bench_gemv(qmm, hipr, stream, max(10, args.steps // 4), max(3, args.warmup // 4), N=11008, K=4096,
@@ -647,7 +648,8 @@ def main(argv=None) -> int:
         prefill.append({"workload": f"q8_0_linear_n11008_k4096_m{m_short}_f32x", "unit": "TFLOP/s",
                         "value": round(rl["tflops_kernel"], 2), "kernel_us": round(rl["kernel_ms"] * 1e3, 3),
                         "frac": round(rl["tflops_kernel"] / BF16_PEAK_TFLOPS, 4),
-                        "route": "fp32 GEMM (openmini_qmm_gemm_min_rows = 64 on this weight)",
+                        "route": ("fp32 GEMM" if m_short >= rl["gemm_min_rows"] else "decode GEMVs"),
+                        "gemm_min_rows": rl["gemm_min_rows"],
                         "gemv_passes_us": round(gl["kernel_ms"] * 1e3, 3),
                         "launch_shape": rl["launch_shape"], "sha256": rl["sha256"]})
         log(f"q8_0 linear M={m_short} f32 x: GEMM {rl['kernel_ms'] * 1e3:.2f} us vs GEMV passes "
